@@ -1,0 +1,255 @@
+// FP32 GEMM on gfx950 f32 MFMA (v_mfma_f32_16x16x4_f32):
+//   C = alpha * op(A) * op(B) + beta * C, row-major, all four transposes.
+//
+// Block tile 128 x 128 x 32, 4 waves (2 x 2), each wave a 64 x 64 sub-tile of
+// 4 x 4 MFMA blocks.  Tiles are copied HBM -> registers -> LDS unchanged
+// (128-bit loads along each operand's contiguous dimension, double-buffered
+// LDS), and every MFMA operand is then fetched with one ds_read_b128 that
+// serves four MFMAs:
+//   * an operand stored k-contiguous (A as [M,K], B as [N,K]) is read as
+//     4 consecutive k of one row   -> the 4 k-substeps of a 16-k slice;
+//   * an operand stored row-contiguous (A as [K,M], B as [K,N]) is read as
+//     4 consecutive rows of one k  -> the 4 MFMA blocks of the wave, whose
+//     rows are then interleaved (block f owns rows f, f+4, f+8, ...).
+// Both give lane l the k index 4*(l/16) + s of substep s, so A and B agree.
+// With B stored [K,N] the interleaved output columns make every lane own 4
+// consecutive columns, so C is read and written with 128-bit accesses.
+#include "common.h"
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int kThreads = 256;
+constexpr int TM = 64, TN = 64;  // wave tile
+constexpr int FM = 4, FN = 4;    // 16x16 MFMA blocks per wave tile
+constexpr int kPadK = BK + 4;    // pitch (floats) of a k-contiguous LDS tile
+constexpr int kPadR = BM + 4;    // pitch (floats) of a row-contiguous LDS tile
+constexpr int kTileFloats = (BM * kPadK > BK * kPadR) ? BM * kPadK : BK * kPadR;
+constexpr int kLoads = BM * BK / 4 / kThreads;  // float4 per thread per operand
+
+// Operand geometry: a tile of R rows (M or N) by BK k-values.  KCONTIG: the
+// global matrix is [R_total, K] (k contiguous), else [K, R_total].
+template <bool KCONTIG, bool VEC>
+struct Operand {
+    const float* __restrict__ base;
+    uint32_t ld, rows, K;
+
+    // Chunk c of the tile -> (tile row, tile k) of its first element.
+    __device__ __forceinline__ static void chunk_pos(uint32_t c, uint32_t& r, uint32_t& k) {
+        if (KCONTIG) {
+            r = c / (BK / 4);
+            k = (c % (BK / 4)) * 4;
+        } else {
+            k = c / (BM / 4);
+            r = (c % (BM / 4)) * 4;
+        }
+    }
+
+    __device__ __forceinline__ float4 load(uint32_t r0, uint32_t k0, uint32_t c) const {
+        uint32_t r, k;
+        chunk_pos(c, r, k);
+        r += r0;
+        k += k0;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (KCONTIG) {
+            if (r >= rows) return v;
+            const float* p = base + (uint64_t)r * ld + k;
+            if (VEC) {
+                if (k < K) v = *reinterpret_cast<const float4*>(p);
+            } else {
+                v.x = k + 0 < K ? p[0] : 0.f;
+                v.y = k + 1 < K ? p[1] : 0.f;
+                v.z = k + 2 < K ? p[2] : 0.f;
+                v.w = k + 3 < K ? p[3] : 0.f;
+            }
+        } else {
+            if (k >= K) return v;
+            const float* p = base + (uint64_t)k * ld + r;
+            if (VEC) {
+                if (r < rows) v = *reinterpret_cast<const float4*>(p);
+            } else {
+                v.x = r + 0 < rows ? p[0] : 0.f;
+                v.y = r + 1 < rows ? p[1] : 0.f;
+                v.z = r + 2 < rows ? p[2] : 0.f;
+                v.w = r + 3 < rows ? p[3] : 0.f;
+            }
+        }
+        return v;
+    }
+
+    __device__ __forceinline__ static void store(float* s, uint32_t c, float4 v) {
+        uint32_t r, k;
+        chunk_pos(c, r, k);
+        if (KCONTIG)
+            *reinterpret_cast<float4*>(&s[r * kPadK + k]) = v;
+        else
+            *reinterpret_cast<float4*>(&s[k * kPadR + r]) = v;
+    }
+
+    // Fragments for one 16-k slice (kh): frag[f][s] is the value this lane
+    // feeds MFMA block f at substep s.
+    __device__ __forceinline__ static void frags(const float* s, uint32_t wofs, uint32_t lane, int kh,
+                                                 float frag[4][4]) {
+        const uint32_t kg = lane / 16, li = lane % 16;
+        if (KCONTIG) {
+#pragma unroll
+            for (int f = 0; f < 4; f++) {
+                float4 v = *reinterpret_cast<const float4*>(&s[(wofs + f * 16 + li) * kPadK + kh * 16 + 4 * kg]);
+                frag[f][0] = v.x;
+                frag[f][1] = v.y;
+                frag[f][2] = v.z;
+                frag[f][3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int sub = 0; sub < 4; sub++) {
+                float4 v = *reinterpret_cast<const float4*>(&s[(kh * 16 + 4 * kg + sub) * kPadR + wofs + li * 4]);
+                frag[0][sub] = v.x;
+                frag[1][sub] = v.y;
+                frag[2][sub] = v.z;
+                frag[3][sub] = v.w;
+            }
+        }
+    }
+
+    // Tile-relative row of MFMA block f, in-block index i (0..15).
+    __device__ __forceinline__ static uint32_t row_of(uint32_t wofs, int f, uint32_t i) {
+        return KCONTIG ? wofs + f * 16 + i : wofs + i * 4 + f;
+    }
+};
+
+template <bool TA, bool TB, bool VEC>
+__global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, uint32_t K, float alpha,
+                                                       const float* __restrict__ A, uint32_t lda,
+                                                       const float* __restrict__ B, uint32_t ldb, float beta,
+                                                       float* __restrict__ C, uint32_t ldc) {
+    using OpA = Operand<!TA, VEC>;
+    using OpB = Operand<TB, VEC>;
+    __shared__ __attribute__((aligned(16))) float As[2][kTileFloats];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kTileFloats];
+
+    const OpA opa{A, lda, M, K};
+    const OpB opb{B, ldb, N, K};
+    const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const uint32_t wm = (wave / 2) * TM, wn = (wave % 2) * TN;
+    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    v4f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    float4 ra[kLoads], rb[kLoads];
+    auto gload = [&](uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < kLoads; i++) ra[i] = opa.load(m0, k0, tid + i * kThreads);
+#pragma unroll
+        for (int i = 0; i < kLoads; i++) rb[i] = opb.load(n0, k0, tid + i * kThreads);
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < kLoads; i++) OpA::store(As[buf], tid + i * kThreads, ra[i]);
+#pragma unroll
+        for (int i = 0; i < kLoads; i++) OpB::store(Bs[buf], tid + i * kThreads, rb[i]);
+    };
+
+    const uint32_t nk = (K + BK - 1) / BK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (uint32_t kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload((kt + 1) * BK);
+#pragma unroll
+        for (int kh = 0; kh < BK / 16; kh++) {
+            float fa[4][4], fb[4][4];
+            OpA::frags(As[buf], wm, lane, kh, fa);
+            OpB::frags(Bs[buf], wn, lane, kh, fb);
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: lane owns column lane%16 and rows 4*(lane/16)+r of each block.
+    const uint32_t li = lane % 16, rg = 4 * (lane / 16);
+    if (!TB && VEC) {
+        // Interleaved columns: block j holds column li*4 + j -> 4 consecutive
+        // columns per lane, one float4 read-modify-write per (i, r).
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                uint32_t m = m0 + OpA::row_of(wm, i, rg + r);
+                uint32_t n = n0 + wn + li * 4;
+                if (m >= M || n >= N) continue;
+                float4* cp = reinterpret_cast<float4*>(&C[(uint64_t)m * ldc + n]);
+                float4 c = *cp;
+                c.x = alpha * acc[i][0][r] + beta * c.x;
+                c.y = alpha * acc[i][1][r] + beta * c.y;
+                c.z = alpha * acc[i][2][r] + beta * c.z;
+                c.w = alpha * acc[i][3][r] + beta * c.w;
+                *cp = c;
+            }
+    } else {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    uint32_t m = m0 + OpA::row_of(wm, i, rg + r);
+                    uint32_t n = n0 + OpB::row_of(wn, j, li);
+                    if (m < M && n < N) {
+                        float* cp = &C[(uint64_t)m * ldc + n];
+                        *cp = alpha * acc[i][j][r] + beta * *cp;
+                    }
+                }
+    }
+}
+
+bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
+
+template <bool TA, bool TB>
+int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint32_t lda, const float* B,
+           uint32_t ldb, float beta, float* C, uint32_t ldc, hipStream_t s) {
+    // 128-bit paths need the contiguous extents and leading dimensions to be
+    // multiples of 4 floats and 16-byte aligned bases.
+    bool vec = aligned16(A) && aligned16(B) && aligned16(C) && lda % 4 == 0 && ldb % 4 == 0 &&
+               ldc % 4 == 0 && N % 4 == 0 && (TA ? M % 4 == 0 : K % 4 == 0) && (TB ? K % 4 == 0 : true);
+    dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+    if (grid.y > 65535) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "sgemm: M=%u too large", M);
+    if (vec)
+        hipLaunchKernelGGL((k_sgemm<TA, TB, true>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B, ldb,
+                           beta, C, ldc);
+    else
+        hipLaunchKernelGGL((k_sgemm<TA, TB, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B, ldb,
+                           beta, C, ldc);
+    return rplhip::check_launch("sgemm");
+}
+
+}  // namespace
+
+using namespace rplhip;
+
+extern "C" int rplhip_sgemm(int trans_a, int trans_b, uint32_t M, uint32_t N, uint32_t K, float alpha,
+                            const float* A, uint32_t lda, const float* B, uint32_t ldb, float beta, float* C,
+                            uint32_t ldc, rplhip_stream_t stream) {
+    if (M == 0 || N == 0) return RPLHIP_OK;
+    if (!C || (K && (!A || !B))) return fail(RPLHIP_ERR_INVALID, "rplhip_sgemm: NULL pointer");
+    if (ldc < N || (K && (lda < (trans_a ? M : K) || ldb < (trans_b ? K : N))))
+        return fail(RPLHIP_ERR_INVALID, "rplhip_sgemm: leading dimension too small");
+    RPLHIP_REQUIRE_DEVICE();
+    hipStream_t s = as_stream(stream);
+    if (!trans_a && !trans_b) return launch<false, false>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
+    if (!trans_a && trans_b) return launch<false, true>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
+    if (trans_a && !trans_b) return launch<true, false>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
+    return launch<true, true>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
+}

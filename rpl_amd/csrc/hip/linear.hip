@@ -1,0 +1,261 @@
+// Elementwise and reduction kernels around the Linear GEMMs: bias add (+ReLU),
+// ReLU backward, gradient accumulation, the bias-gradient column reduction and
+// the MSE loss / backward.  All are HBM- or launch-bound; the GEMMs dominate.
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxBlocks = 2048;
+
+int grid_for(uint64_t items) {
+    uint64_t b = (items + kThreads - 1) / kThreads;
+    if (b < 1) b = 1;
+    return (int)(b < (uint64_t)kMaxBlocks ? b : (uint64_t)kMaxBlocks);
+}
+
+#define GRID_STRIDE(i, n)                                                          \
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (n); \
+         i += (uint64_t)gridDim.x * blockDim.x)
+
+// out[i] = a[i] + b[i % nb]; act[i] = relu(out[i]) when act != NULL
+// (rpl_core.c:112-120 then :291).
+__global__ void __launch_bounds__(kThreads) k_bias_add_relu(const float* __restrict__ a,
+                                                            const float* __restrict__ b,
+                                                            float* __restrict__ out,
+                                                            float* __restrict__ act, uint64_t n,
+                                                            uint64_t nb) {
+    GRID_STRIDE(i, n) {
+        float v = a[i] + b[i % nb];
+        out[i] = v;
+        if (act) act[i] = v > 0 ? v : 0;
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) k_relu(const float* __restrict__ x, float* __restrict__ y,
+                                                   uint64_t n) {
+    GRID_STRIDE(i, n) {
+        float v = x[i];
+        y[i] = v > 0 ? v : 0;
+    }
+}
+
+// rpl_core.c:421
+__global__ void __launch_bounds__(kThreads) k_relu_backward(const float* __restrict__ x,
+                                                            const float* __restrict__ dy,
+                                                            float* __restrict__ dx, uint64_t n) {
+    GRID_STRIDE(i, n) {
+        if (x[i] > 0) dx[i] += dy[i];
+    }
+}
+
+// rpl_core.c:324
+__global__ void __launch_bounds__(kThreads) k_accumulate(const float* __restrict__ dy,
+                                                         float* __restrict__ dx, uint64_t n) {
+    GRID_STRIDE(i, n) { dx[i] += dy[i]; }
+}
+
+__global__ void __launch_bounds__(kThreads) k_fill(float* __restrict__ x, uint64_t n, float v) {
+    GRID_STRIDE(i, n) { x[i] = v; }
+}
+
+// Bias-gradient column reduction, stage 1: dy viewed as [rows, nb]; block
+// (cx, split) sums 64 columns over its slice of rows with 4 row lanes, so
+// each wave reads 64 consecutive floats of a row (coalesced).
+constexpr int kColTile = 64;
+constexpr int kRowLanes = kThreads / kColTile;
+
+__global__ void __launch_bounds__(kThreads) k_colsum_partial(const float* __restrict__ dy, uint64_t n,
+                                                             uint64_t rows, uint64_t nb,
+                                                             uint64_t rows_per_split,
+                                                             float* __restrict__ part) {
+    __shared__ float red[kRowLanes][kColTile];
+    uint64_t c = (uint64_t)blockIdx.x * kColTile + threadIdx.x % kColTile;
+    int lane_r = threadIdx.x / kColTile;
+    uint64_t r0 = (uint64_t)blockIdx.y * rows_per_split;
+    uint64_t r1 = r0 + rows_per_split < rows ? r0 + rows_per_split : rows;
+    float g = 0;
+    if (c < nb)
+        for (uint64_t r = r0 + lane_r; r < r1; r += kRowLanes)
+            if (r * nb + c < n) g += dy[r * nb + c];
+    red[lane_r][threadIdx.x % kColTile] = g;
+    __syncthreads();
+    if (lane_r == 0 && c < nb) {
+        float s = red[0][threadIdx.x];
+        for (int k = 1; k < kRowLanes; k++) s += red[k][threadIdx.x];
+        part[(uint64_t)blockIdx.y * nb + c] = s;
+    }
+}
+
+// Stage 2: db[c] += sum over splits (rpl_core.c:333).
+__global__ void __launch_bounds__(kThreads) k_colsum_finish(const float* __restrict__ part, int splits,
+                                                            uint64_t nb, float* __restrict__ db) {
+    GRID_STRIDE(c, nb) {
+        float s = 0;
+        for (int k = 0; k < splits; k++) s += part[(uint64_t)k * nb + c];
+        db[c] += s;
+    }
+}
+
+// MSE: per-block partial sums of (p - t)^2, then one block finishes.
+__device__ float block_sum(float v) {
+    __shared__ float s[kThreads / 64];
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    if (threadIdx.x % 64 == 0) s[threadIdx.x / 64] = v;
+    __syncthreads();
+    float t = 0;
+    for (int i = 0; i < (int)(blockDim.x / 64); i++) t += s[i];
+    __syncthreads();
+    return t;
+}
+
+__global__ void __launch_bounds__(kThreads) k_sqerr_partial(const float* __restrict__ p,
+                                                            const float* __restrict__ t, uint64_t n,
+                                                            float* __restrict__ part) {
+    float acc = 0;
+    GRID_STRIDE(i, n) {
+        float d = p[i] - t[i];
+        acc += d * d;
+    }
+    acc = block_sum(acc);
+    if (threadIdx.x == 0) part[blockIdx.x] = acc;
+}
+
+__global__ void __launch_bounds__(kThreads) k_sqerr_finish(const float* __restrict__ part, int nparts,
+                                                           uint64_t n, float* __restrict__ loss) {
+    float acc = 0;
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x) acc += part[i];
+    acc = block_sum(acc);
+    if (threadIdx.x == 0) loss[0] = acc / (float)n;  // rpl_core.c:457
+}
+
+// rpl_core.c:441-444
+__global__ void __launch_bounds__(kThreads) k_mse_backward(const float* __restrict__ p,
+                                                           const float* __restrict__ t, uint64_t n,
+                                                           const float* __restrict__ g0p,
+                                                           float* __restrict__ dp) {
+    float factor = 2.0f / (float)n;
+    float g0 = *g0p;
+    GRID_STRIDE(i, n) { dp[i] += g0 * factor * (p[i] - t[i]); }
+}
+
+}  // namespace
+
+using namespace rplhip;
+
+#define NEED(cond, name)                                                     \
+    do {                                                                     \
+        if (!(cond)) return fail(RPLHIP_ERR_INVALID, name ": NULL pointer"); \
+    } while (0)
+
+extern "C" {
+
+int rplhip_add_broadcast(const float* a, const float* b, float* out, uint64_t n, uint64_t nb,
+                         rplhip_stream_t stream) {
+    return rplhip_bias_add_relu(a, b, out, nullptr, n, nb, stream);
+}
+
+int rplhip_bias_add_relu(const float* mm, const float* b, float* out, float* act, uint64_t n,
+                         uint64_t nb, rplhip_stream_t stream) {
+    if (n == 0) return RPLHIP_OK;
+    NEED(mm && b && out, "rplhip_bias_add_relu");
+    if (nb == 0) return fail(RPLHIP_ERR_INVALID, "rplhip_bias_add_relu: broadcast size is 0");
+    RPLHIP_REQUIRE_DEVICE();
+    hipLaunchKernelGGL(k_bias_add_relu, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), mm, b,
+                       out, act, n, nb);
+    return check_launch("bias_add_relu");
+}
+
+int rplhip_relu(const float* x, float* y, uint64_t n, rplhip_stream_t stream) {
+    if (n == 0) return RPLHIP_OK;
+    NEED(x && y, "rplhip_relu");
+    RPLHIP_REQUIRE_DEVICE();
+    hipLaunchKernelGGL(k_relu, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), x, y, n);
+    return check_launch("relu");
+}
+
+int rplhip_relu_backward(const float* x, const float* dy, float* dx, uint64_t n,
+                         rplhip_stream_t stream) {
+    if (n == 0) return RPLHIP_OK;
+    NEED(x && dy && dx, "rplhip_relu_backward");
+    RPLHIP_REQUIRE_DEVICE();
+    hipLaunchKernelGGL(k_relu_backward, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), x, dy,
+                       dx, n);
+    return check_launch("relu_backward");
+}
+
+int rplhip_accumulate(const float* dy, float* dx, uint64_t n, rplhip_stream_t stream) {
+    if (n == 0) return RPLHIP_OK;
+    NEED(dy && dx, "rplhip_accumulate");
+    RPLHIP_REQUIRE_DEVICE();
+    hipLaunchKernelGGL(k_accumulate, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), dy, dx, n);
+    return check_launch("accumulate");
+}
+
+int rplhip_fill(float* x, uint64_t n, float value, rplhip_stream_t stream) {
+    if (n == 0) return RPLHIP_OK;
+    NEED(x, "rplhip_fill");
+    RPLHIP_REQUIRE_DEVICE();
+    hipLaunchKernelGGL(k_fill, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), x, n, value);
+    return check_launch("fill");
+}
+
+int rplhip_bias_grad(const float* dy, uint64_t n, float* db, uint64_t nb, rplhip_stream_t stream) {
+    if (nb == 0) return RPLHIP_OK;
+    NEED(dy && db, "rplhip_bias_grad");
+    RPLHIP_REQUIRE_DEVICE();
+    hipStream_t s = as_stream(stream);
+    // backward_add's j-loop visits i, i+nb, ... < n: ceil(n/nb) rows.
+    uint64_t full_rows = (n + nb - 1) / nb;
+    uint64_t cx = (nb + kColTile - 1) / kColTile;
+    // Enough row splits to put ~4 blocks on every CU, each split >= 64 rows.
+    uint64_t want = (4ull * cu_count() + cx - 1) / cx;
+    uint64_t splits = full_rows / 64;
+    if (splits > want) splits = want;
+    if (splits < 1) splits = 1;
+    if (splits > 65535) splits = 65535;
+    uint64_t rps = (full_rows + splits - 1) / splits;
+    splits = (full_rows + rps - 1) / rps;
+    if (splits < 1) splits = 1;
+    void* ws = nullptr;
+    int st = ws_alloc(&ws, sizeof(float) * splits * nb, s);
+    if (st) return st;
+    // A ragged last row (n % nb != 0, columns < n % nb get one more term) is
+    // handled by the r*nb + c < n bound in the partial kernel.
+    hipLaunchKernelGGL(k_colsum_partial, dim3((unsigned)cx, (unsigned)splits), dim3(kThreads), 0, s, dy, n,
+                       full_rows, nb, rps, (float*)ws);
+    hipLaunchKernelGGL(k_colsum_finish, dim3(grid_for(nb)), dim3(kThreads), 0, s, (const float*)ws,
+                       (int)splits, nb, db);
+    st = check_launch("bias_grad");
+    ws_free(ws, s);
+    return st;
+}
+
+int rplhip_mse_loss(const float* pred, const float* target, uint64_t n, float* loss,
+                    rplhip_stream_t stream) {
+    NEED(pred && target && loss, "rplhip_mse_loss");
+    RPLHIP_REQUIRE_DEVICE();
+    hipStream_t s = as_stream(stream);
+    int g = grid_for(n);
+    if (g > 1024) g = 1024;
+    void* ws = nullptr;
+    int st = ws_alloc(&ws, sizeof(float) * g, s);
+    if (st) return st;
+    hipLaunchKernelGGL(k_sqerr_partial, dim3(g), dim3(kThreads), 0, s, pred, target, n, (float*)ws);
+    hipLaunchKernelGGL(k_sqerr_finish, dim3(1), dim3(kThreads), 0, s, (const float*)ws, g, n, loss);
+    st = check_launch("mse_loss");
+    ws_free(ws, s);
+    return st;
+}
+
+int rplhip_mse_backward(const float* pred, const float* target, uint64_t n, const float* g0,
+                        float* dpred, rplhip_stream_t stream) {
+    if (n == 0) return RPLHIP_OK;
+    NEED(pred && target && g0 && dpred, "rplhip_mse_backward");
+    RPLHIP_REQUIRE_DEVICE();
+    hipLaunchKernelGGL(k_mse_backward, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), pred,
+                       target, n, g0, dpred);
+    return check_launch("mse_backward");
+}
+
+}  // extern "C"

@@ -1,0 +1,384 @@
+// Quantize / dequantize / min-max kernels (bit-exact with the reference).
+//
+// All of these are HBM-bound streaming passes: 128-bit loads and stores,
+// grid-stride loops sized to fill the 256 CUs, and deterministic two-stage
+// reductions (per-block partials in a stream-ordered workspace, then one
+// finishing block) instead of float atomics.
+#include <float.h>
+#include <math.h>
+
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxBlocks = 1024;
+
+__device__ __forceinline__ float sel_min(float v, float m) { return v < m ? v : m; }
+__device__ __forceinline__ float sel_max(float v, float m) { return v > m ? v : m; }
+
+// Block-wide reduction of (min, max) with NaN never selected; every thread
+// gets the result.
+__device__ void block_min_max(float& mn, float& mx) {
+    __shared__ float smin[kThreads / 64], smax[kThreads / 64];
+    for (int off = 32; off > 0; off >>= 1) {
+        mn = sel_min(__shfl_xor(mn, off), mn);
+        mx = sel_max(__shfl_xor(mx, off), mx);
+    }
+    int w = threadIdx.x / 64, l = threadIdx.x % 64;
+    if (l == 0) { smin[w] = mn; smax[w] = mx; }
+    __syncthreads();
+    mn = smin[0];
+    mx = smax[0];
+    for (int i = 1; i < (int)(blockDim.x / 64); i++) {
+        mn = sel_min(smin[i], mn);
+        mx = sel_max(smax[i], mx);
+    }
+    __syncthreads();
+}
+
+// Stage 1: per-block (min, max) of x[0..n), OpenMP-reduction semantics.
+__global__ void __launch_bounds__(kThreads) k_min_max_partial(const float* __restrict__ x, uint64_t n,
+                                                              float2* __restrict__ part) {
+    float mn = FLT_MAX, mx = -FLT_MAX;
+    uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    bool vec = (((uintptr_t)x) & 15) == 0;
+    if (vec) {
+        uint64_t n4 = n / 4;
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        for (uint64_t i = tid; i < n4; i += stride) {
+            float4 v = x4[i];
+            mn = sel_min(v.x, mn); mx = sel_max(v.x, mx);
+            mn = sel_min(v.y, mn); mx = sel_max(v.y, mx);
+            mn = sel_min(v.z, mn); mx = sel_max(v.z, mx);
+            mn = sel_min(v.w, mn); mx = sel_max(v.w, mx);
+        }
+        for (uint64_t i = n4 * 4 + tid; i < n; i += stride) {
+            mn = sel_min(x[i], mn);
+            mx = sel_max(x[i], mx);
+        }
+    } else {
+        for (uint64_t i = tid; i < n; i += stride) {
+            mn = sel_min(x[i], mn);
+            mx = sel_max(x[i], mx);
+        }
+    }
+    block_min_max(mn, mx);
+    if (threadIdx.x == 0) part[blockIdx.x] = make_float2(mn, mx);
+}
+
+// Which parameters the finishing block derives from the global (min, max).
+enum Finish { kMinMax = 0, kSymmetric = 1, kAsymmetric = 2 };
+
+// Stage 2 (one block): combine partials and derive the quantization params.
+//   kMinMax:     out2 = {min, max}
+//   kSymmetric:  scale = fmaxf(fabsf(min), fabsf(max)) / 127  (rpl_quantization.c:87-88)
+//   kAsymmetric: scale = (max - min) / 255, zp = (int32)roundf(-min / scale)  (:102-104)
+template <int F>
+__global__ void __launch_bounds__(kThreads) k_min_max_finish(const float2* __restrict__ part, int nparts,
+                                                             float* __restrict__ out_f,
+                                                             int32_t* __restrict__ out_zp) {
+    float mn = FLT_MAX, mx = -FLT_MAX;
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+        float2 p = part[i];
+        mn = sel_min(p.x, mn);
+        mx = sel_max(p.y, mx);
+    }
+    block_min_max(mn, mx);
+    if (threadIdx.x != 0) return;
+    if (F == kMinMax) {
+        out_f[0] = mn;
+        out_f[1] = mx;
+    } else if (F == kSymmetric) {
+        float abs_max = fmaxf(fabsf(mn), fabsf(mx));
+        out_f[0] = abs_max / 127.0f;
+    } else {
+        float range = mx - mn;
+        float scale = range / 255.0f;
+        out_f[0] = scale;
+        out_zp[0] = x86_cvt_i32(roundf(-mn / scale));
+    }
+}
+
+// q = quantize_one(x, scale, zp); scale / zp come from device memory when
+// the pointers are given (symmetric / asymmetric chains), else the values.
+__global__ void __launch_bounds__(kThreads) k_quantize(const float* __restrict__ x, uint64_t n,
+                                                       float scale_v, int32_t zp_v,
+                                                       const float* __restrict__ scale_p,
+                                                       const int32_t* __restrict__ zp_p,
+                                                       int8_t* __restrict__ q) {
+    float scale = scale_p ? *scale_p : scale_v;
+    int32_t zp = zp_p ? *zp_p : zp_v;
+    uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    bool vec = ((((uintptr_t)x) & 15) == 0) && ((((uintptr_t)q) & 3) == 0);
+    uint64_t n4 = vec ? n / 4 : 0;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    uint32_t* q4 = reinterpret_cast<uint32_t*>(q);
+    for (uint64_t i = tid; i < n4; i += stride) {
+        float4 v = x4[i];
+        uint32_t b0 = (uint8_t)quantize_one(v.x, scale, zp);
+        uint32_t b1 = (uint8_t)quantize_one(v.y, scale, zp);
+        uint32_t b2 = (uint8_t)quantize_one(v.z, scale, zp);
+        uint32_t b3 = (uint8_t)quantize_one(v.w, scale, zp);
+        q4[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    }
+    for (uint64_t i = n4 * 4 + tid; i < n; i += stride) q[i] = quantize_one(x[i], scale, zp);
+}
+
+// y = (float)(q - zp) * scale  (ops_extended.c:69)
+__global__ void __launch_bounds__(kThreads) k_dequantize(const int8_t* __restrict__ q, uint64_t n,
+                                                         float scale, int32_t zp,
+                                                         float* __restrict__ y) {
+    uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    bool vec = ((((uintptr_t)q) & 3) == 0) && ((((uintptr_t)y) & 15) == 0);
+    uint64_t n4 = vec ? n / 4 : 0;
+    const uint32_t* q4 = reinterpret_cast<const uint32_t*>(q);
+    float4* y4 = reinterpret_cast<float4*>(y);
+    for (uint64_t i = tid; i < n4; i += stride) {
+        uint32_t w = q4[i];
+        float4 o;
+        o.x = (float)((int32_t)(int8_t)(w & 0xff) - zp) * scale;
+        o.y = (float)((int32_t)(int8_t)((w >> 8) & 0xff) - zp) * scale;
+        o.z = (float)((int32_t)(int8_t)((w >> 16) & 0xff) - zp) * scale;
+        o.w = (float)((int32_t)(int8_t)(w >> 24) - zp) * scale;
+        y4[i] = o;
+    }
+    for (uint64_t i = n4 * 4 + tid; i < n; i += stride) y[i] = (float)((int32_t)q[i] - zp) * scale;
+}
+
+// Per-channel (per-row) symmetric quantization, one block per slice:
+// min/max over the slice, scale = fmaxf(|min|,|max|)/127, then quantize.
+// Slices of up to kRegItems*4*kThreads floats with 16-byte aligned rows are
+// held in registers, so the slice is read from HBM once.
+constexpr int kRegItems = 8;  // float4 per thread -> 8192 floats per slice
+template <bool REG>
+__global__ void __launch_bounds__(kThreads) k_quantize_rows(const float* __restrict__ x, uint32_t rows,
+                                                            uint32_t cols, int8_t* __restrict__ q,
+                                                            float* __restrict__ scales) {
+    uint32_t r = blockIdx.x;
+    const float* xr = x + (uint64_t)r * cols;
+    int8_t* qr = q + (uint64_t)r * cols;
+    float mn = FLT_MAX, mx = -FLT_MAX;
+    if (REG) {
+        float4 v[kRegItems];
+        const float4* x4 = reinterpret_cast<const float4*>(xr);
+        uint32_t n4 = cols / 4;
+#pragma unroll
+        for (int it = 0; it < kRegItems; it++) {
+            uint32_t i = threadIdx.x + it * kThreads;
+            if (i < n4) {
+                v[it] = x4[i];
+                mn = sel_min(v[it].x, mn); mx = sel_max(v[it].x, mx);
+                mn = sel_min(v[it].y, mn); mx = sel_max(v[it].y, mx);
+                mn = sel_min(v[it].z, mn); mx = sel_max(v[it].z, mx);
+                mn = sel_min(v[it].w, mn); mx = sel_max(v[it].w, mx);
+            }
+        }
+        block_min_max(mn, mx);
+        float scale = fmaxf(fabsf(mn), fabsf(mx)) / 127.0f;
+        if (threadIdx.x == 0) scales[r] = scale;
+        uint32_t* q4 = reinterpret_cast<uint32_t*>(qr);
+#pragma unroll
+        for (int it = 0; it < kRegItems; it++) {
+            uint32_t i = threadIdx.x + it * kThreads;
+            if (i < n4) {
+                uint32_t b0 = (uint8_t)quantize_one(v[it].x, scale, 0);
+                uint32_t b1 = (uint8_t)quantize_one(v[it].y, scale, 0);
+                uint32_t b2 = (uint8_t)quantize_one(v[it].z, scale, 0);
+                uint32_t b3 = (uint8_t)quantize_one(v[it].w, scale, 0);
+                q4[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            }
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < cols; i += kThreads) {
+            mn = sel_min(xr[i], mn);
+            mx = sel_max(xr[i], mx);
+        }
+        block_min_max(mn, mx);
+        float scale = fmaxf(fabsf(mn), fabsf(mx)) / 127.0f;
+        if (threadIdx.x == 0) scales[r] = scale;
+        for (uint32_t i = threadIdx.x; i < cols; i += kThreads) qr[i] = quantize_one(xr[i], scale, 0);
+    }
+}
+
+// tensor_get_min_max: first index attaining the extreme wins.
+struct ArgExt {
+    float mn;
+    uint64_t imn;
+    float mx;
+    uint64_t imx;
+};
+
+__device__ __forceinline__ void argext_merge(ArgExt& a, float vmn, uint64_t imn, float vmx,
+                                             uint64_t imx) {
+    if (vmn < a.mn || (vmn == a.mn && imn < a.imn)) { a.mn = vmn; a.imn = imn; }
+    if (vmx > a.mx || (vmx == a.mx && imx < a.imx)) { a.mx = vmx; a.imx = imx; }
+}
+
+__device__ void block_argext(ArgExt& a) {
+    __shared__ ArgExt s[kThreads / 64];
+    for (int off = 32; off > 0; off >>= 1) {
+        float vmn = __shfl_xor(a.mn, off);
+        uint64_t imn = __shfl_xor(a.imn, off);
+        float vmx = __shfl_xor(a.mx, off);
+        uint64_t imx = __shfl_xor(a.imx, off);
+        argext_merge(a, vmn, imn, vmx, imx);
+    }
+    int w = threadIdx.x / 64;
+    if (threadIdx.x % 64 == 0) s[w] = a;
+    __syncthreads();
+    a = s[0];
+    for (int i = 1; i < (int)(blockDim.x / 64); i++) argext_merge(a, s[i].mn, s[i].imn, s[i].mx, s[i].imx);
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(kThreads) k_argext_partial(const float* __restrict__ x, uint64_t n,
+                                                             ArgExt* __restrict__ part) {
+    ArgExt a = {__builtin_huge_valf(), ~0ull, -__builtin_huge_valf(), ~0ull};
+    uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = tid; i < n; i += stride) {
+        float v = x[i];
+        if (v == v) argext_merge(a, v, i, v, i);  // NaN never selected past x[0]
+    }
+    block_argext(a);
+    if (threadIdx.x == 0) part[blockIdx.x] = a;
+}
+
+__global__ void __launch_bounds__(kThreads) k_argext_finish(const float* __restrict__ x,
+                                                            const ArgExt* __restrict__ part,
+                                                            int nparts, float* __restrict__ out2) {
+    ArgExt a = {__builtin_huge_valf(), ~0ull, -__builtin_huge_valf(), ~0ull};
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x)
+        argext_merge(a, part[i].mn, part[i].imn, part[i].mx, part[i].imx);
+    block_argext(a);
+    if (threadIdx.x != 0) return;
+    float x0 = x[0];
+    if (x0 != x0) {  // the scan starts from x[0]; a NaN there is never replaced
+        out2[0] = x0;
+        out2[1] = x0;
+        return;
+    }
+    // All elements are compared against x[0] first, so a non-NaN x[0] is a
+    // candidate; the merged arg-extremes already include it (index 0).
+    out2[0] = x[a.imn];
+    out2[1] = x[a.imx];
+}
+
+int grid_for(uint64_t work_items) {
+    uint64_t b = (work_items + kThreads - 1) / kThreads;
+    if (b < 1) b = 1;
+    int cap = kMaxBlocks;
+    return (int)(b < (uint64_t)cap ? b : (uint64_t)cap);
+}
+
+// Shared two-stage min/max with a finishing mode.
+template <int F>
+int min_max_chain(const float* x, uint64_t n, float* out_f, int32_t* out_zp, hipStream_t s) {
+    int g = grid_for((n + 3) / 4);
+    void* ws = nullptr;
+    int st = rplhip::ws_alloc(&ws, sizeof(float2) * g, s);
+    if (st) return st;
+    hipLaunchKernelGGL(k_min_max_partial, dim3(g), dim3(kThreads), 0, s, x, n, (float2*)ws);
+    hipLaunchKernelGGL(k_min_max_finish<F>, dim3(1), dim3(kThreads), 0, s, (const float2*)ws, g,
+                       out_f, out_zp);
+    st = rplhip::check_launch("min/max reduction");
+    rplhip::ws_free(ws, s);
+    return st;
+}
+
+}  // namespace
+
+using namespace rplhip;
+
+extern "C" {
+
+int rplhip_quantize_int8(const float* x, uint64_t n, float scale, int32_t zp, int8_t* q,
+                         rplhip_stream_t stream) {
+    if (n == 0) return RPLHIP_OK;
+    if (!x || !q) return fail(RPLHIP_ERR_INVALID, "rplhip_quantize_int8: NULL pointer");
+    RPLHIP_REQUIRE_DEVICE();
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(k_quantize, dim3(grid_for((n + 3) / 4)), dim3(kThreads), 0, s, x, n, scale, zp,
+                       (const float*)nullptr, (const int32_t*)nullptr, q);
+    return check_launch("quantize_int8");
+}
+
+int rplhip_min_max(const float* x, uint64_t n, float* out2, rplhip_stream_t stream) {
+    if (!x || !out2) return fail(RPLHIP_ERR_INVALID, "rplhip_min_max: NULL pointer");
+    RPLHIP_REQUIRE_DEVICE();
+    return min_max_chain<kMinMax>(x, n, out2, nullptr, as_stream(stream));
+}
+
+int rplhip_quantize_symmetric(const float* x, uint64_t n, int8_t* q, float* scale_out,
+                              rplhip_stream_t stream) {
+    if (!x || !q || !scale_out) return fail(RPLHIP_ERR_INVALID, "rplhip_quantize_symmetric: NULL pointer");
+    RPLHIP_REQUIRE_DEVICE();
+    hipStream_t s = as_stream(stream);
+    int st = min_max_chain<kSymmetric>(x, n, scale_out, nullptr, s);
+    if (st || n == 0) return st;
+    hipLaunchKernelGGL(k_quantize, dim3(grid_for((n + 3) / 4)), dim3(kThreads), 0, s, x, n, 0.0f, 0,
+                       (const float*)scale_out, (const int32_t*)nullptr, q);
+    return check_launch("quantize_symmetric");
+}
+
+int rplhip_quantize_asymmetric(const float* x, uint64_t n, int8_t* q, float* scale_out,
+                               int32_t* zp_out, rplhip_stream_t stream) {
+    if (!x || !q || !scale_out || !zp_out)
+        return fail(RPLHIP_ERR_INVALID, "rplhip_quantize_asymmetric: NULL pointer");
+    RPLHIP_REQUIRE_DEVICE();
+    hipStream_t s = as_stream(stream);
+    int st = min_max_chain<kAsymmetric>(x, n, scale_out, zp_out, s);
+    if (st || n == 0) return st;
+    hipLaunchKernelGGL(k_quantize, dim3(grid_for((n + 3) / 4)), dim3(kThreads), 0, s, x, n, 0.0f, 0,
+                       (const float*)scale_out, (const int32_t*)zp_out, q);
+    return check_launch("quantize_asymmetric");
+}
+
+int rplhip_quantize_per_channel(const float* x, uint32_t num_channels, uint32_t channel_size,
+                                int8_t* q, float* scales, rplhip_stream_t stream) {
+    if (num_channels == 0) return RPLHIP_OK;
+    if (!x || !q || !scales) return fail(RPLHIP_ERR_INVALID, "rplhip_quantize_per_channel: NULL pointer");
+    RPLHIP_REQUIRE_DEVICE();
+    hipStream_t s = as_stream(stream);
+    bool reg = channel_size % 4 == 0 && channel_size <= (uint32_t)(kRegItems * 4 * kThreads) &&
+               (((uintptr_t)x) & 15) == 0 && (((uintptr_t)q) & 3) == 0;
+    if (reg)
+        hipLaunchKernelGGL(k_quantize_rows<true>, dim3(num_channels), dim3(kThreads), 0, s, x,
+                           num_channels, channel_size, q, scales);
+    else
+        hipLaunchKernelGGL(k_quantize_rows<false>, dim3(num_channels), dim3(kThreads), 0, s, x,
+                           num_channels, channel_size, q, scales);
+    return check_launch("quantize_per_channel");
+}
+
+int rplhip_dequantize_int8(const int8_t* q, uint64_t n, float scale, int32_t zp, float* y,
+                           rplhip_stream_t stream) {
+    if (n == 0) return RPLHIP_OK;
+    if (!q || !y) return fail(RPLHIP_ERR_INVALID, "rplhip_dequantize_int8: NULL pointer");
+    RPLHIP_REQUIRE_DEVICE();
+    hipLaunchKernelGGL(k_dequantize, dim3(grid_for((n + 3) / 4)), dim3(kThreads), 0, as_stream(stream),
+                       q, n, scale, zp, y);
+    return check_launch("dequantize_int8");
+}
+
+int rplhip_get_min_max(const float* x, uint64_t n, float* out2, rplhip_stream_t stream) {
+    if (n == 0) return RPLHIP_OK;
+    if (!x || !out2) return fail(RPLHIP_ERR_INVALID, "rplhip_get_min_max: NULL pointer");
+    RPLHIP_REQUIRE_DEVICE();
+    hipStream_t s = as_stream(stream);
+    int g = grid_for(n);
+    void* ws = nullptr;
+    int st = ws_alloc(&ws, sizeof(ArgExt) * g, s);
+    if (st) return st;
+    hipLaunchKernelGGL(k_argext_partial, dim3(g), dim3(kThreads), 0, s, x, n, (ArgExt*)ws);
+    hipLaunchKernelGGL(k_argext_finish, dim3(1), dim3(kThreads), 0, s, x, (const ArgExt*)ws, g, out2);
+    st = check_launch("get_min_max");
+    ws_free(ws, s);
+    return st;
+}
+
+}  // extern "C"

@@ -1,0 +1,265 @@
+/*
+ * The Linear layer and the autograd pieces it uses (src/rpl_nn.c:16-83,
+ * src/rpl_core.c:95-135,274-300,319-480) on the gfx950 backend.  The graph
+ * walk is the reference's: each backward_fn accumulates into its parents'
+ * gradients and recurses, depth first.  The arithmetic runs on the device:
+ * dX / dW are f32-MFMA GEMMs with beta = 1 (accumulate), the bias gradient
+ * is a column reduction.
+ */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "rpl_host.h"
+
+static int any_gpu(const Tensor* a, const Tensor* b) { return rpl__is_gpu(a) || (b && rpl__is_gpu(b)); }
+
+/* src/rpl_core.c:95-129 */
+void tensor_add_out(Tensor* out, const Tensor* a, const Tensor* b) {
+    if (!out || !a || !b || b->size == 0) {
+        rpl__bad("tensor_add_out", "bad arguments");
+        return;
+    }
+    if (!rpl_gpu_init()) return;
+    RplStage s = {0};
+    const float* da = rpl__view_data(&s, a, 1, 0);
+    const float* db = rpl__view_data(&s, b, 1, 0);
+    float* dout = rpl__view_data(&s, out, 0, 1);
+    if (!s.err) s.err = !rpl__ok(rplhip_add_broadcast(da, db, dout, out->size, b->size, NULL), "tensor_add_out");
+    rpl__stage_finish(&s);
+    if (out->requires_grad) {
+        out->parent1 = (Tensor*)a;
+        out->parent2 = (Tensor*)b;
+        out->backward_fn = backward_add;
+        out->is_leaf = false;
+    }
+}
+
+/* src/rpl_core.c:131-135 */
+Tensor* tensor_add(const Tensor* a, const Tensor* b) {
+    Tensor* out = tensor_create(a->dims, a->shape, a->requires_grad || b->requires_grad);
+    if (!out) return NULL;
+    if (any_gpu(a, b) && !rpl__attach(out, 0)) return out;
+    tensor_add_out(out, a, b);
+    return out;
+}
+
+void tensor_add_gpu(Tensor* out, const Tensor* a, const Tensor* b) {
+    tensor_to_gpu((Tensor*)a);
+    tensor_to_gpu((Tensor*)b);
+    if (!rpl__is_gpu(out) && !rpl__attach(out, 0)) return;
+    tensor_add_out(out, a, b);
+}
+
+/* src/rpl_core.c:274-300 */
+Tensor* tensor_relu(const Tensor* t) {
+    Tensor* out = tensor_create(t->dims, t->shape, t->requires_grad);
+    if (!out) return NULL;
+    if (rpl__is_gpu(t) && !rpl__attach(out, 0)) return out;
+    if (!rpl_gpu_init()) return out;
+    RplStage s = {0};
+    const float* dx = rpl__view_data(&s, t, 1, 0);
+    float* dy = rpl__view_data(&s, out, 0, 1);
+    if (!s.err) s.err = !rpl__ok(rplhip_relu(dx, dy, t->size, NULL), "tensor_relu");
+    rpl__stage_finish(&s);
+    if (out->requires_grad) {
+        out->parent1 = (Tensor*)t;
+        out->backward_fn = backward_relu;
+        out->is_leaf = false;
+    }
+    return out;
+}
+
+void tensor_relu_gpu(Tensor* out, const Tensor* in) {
+    tensor_to_gpu((Tensor*)in);
+    if (!rpl__is_gpu(out) && !rpl__attach(out, 0)) return;
+    RplStage s = {0};
+    const float* dx = rpl__view_data(&s, in, 1, 0);
+    float* dy = rpl__view_data(&s, out, 0, 1);
+    if (!s.err) s.err = !rpl__ok(rplhip_relu(dx, dy, in->size, NULL), "tensor_relu_gpu");
+    rpl__stage_finish(&s);
+}
+
+/* src/rpl_core.c:449-465 */
+Tensor* tensor_mse_loss(const Tensor* pred, const Tensor* target) {
+    uint32_t shape[1] = {1};
+    Tensor* out = tensor_create(1, shape, pred->requires_grad);
+    if (!out) return NULL;
+    if (any_gpu(pred, target) && !rpl__attach(out, 0)) return out;
+    if (!rpl_gpu_init()) return out;
+    RplStage s = {0};
+    const float* dp = rpl__view_data(&s, pred, 1, 0);
+    const float* dt = rpl__view_data(&s, target, 1, 0);
+    float* dl = rpl__view_data(&s, out, 0, 1);
+    if (!s.err) s.err = !rpl__ok(rplhip_mse_loss(dp, dt, pred->size, dl, NULL), "tensor_mse_loss");
+    rpl__stage_finish(&s);
+    if (out->requires_grad) {
+        out->parent1 = (Tensor*)pred;
+        out->parent2 = (Tensor*)target;
+        out->backward_fn = backward_mse;
+        out->is_leaf = false;
+    }
+    return out;
+}
+
+/* src/rpl_core.c:319-337 */
+void backward_add(Tensor* t) {
+    Tensor* a = t->parent1;
+    Tensor* b = t->parent2;
+    if (a && a->grad) {
+        RplStage s = {0};
+        const float* dy = rpl__view_grad(&s, t, 1, 0);
+        float* da = rpl__view_grad(&s, a, 1, 1);
+        if (!s.err) s.err = !rpl__ok(rplhip_accumulate(dy, da, t->size, NULL), "backward_add");
+        rpl__stage_finish(&s);
+        if (a->backward_fn) a->backward_fn(a);
+    }
+    if (b && b->grad) {
+        RplStage s = {0};
+        const float* dy = rpl__view_grad(&s, t, 1, 0);
+        float* db = rpl__view_grad(&s, b, 1, 1);
+        if (!s.err) s.err = !rpl__ok(rplhip_bias_grad(dy, t->size, db, b->size, NULL), "backward_add (bias)");
+        rpl__stage_finish(&s);
+        if (b->backward_fn) b->backward_fn(b);
+    }
+}
+
+/* src/rpl_core.c:363-416, including its layout guess for B (b is taken as
+ * [N,K] -- the Linear weight layout -- when its shape says so). */
+void backward_matmul(Tensor* t) {
+    Tensor* a = t->parent1;
+    Tensor* b = t->parent2;
+    uint32_t M = t->shape[0], N = t->shape[1], K = a->shape[1];
+    bool b_trans = (b->shape[0] == N && b->shape[1] == K);
+    if (a->grad) {
+        /* dA[M,K] += dt[M,N] * (b_trans ? B[N,K] : B[K,N]^T) */
+        RplStage s = {0};
+        const float* dt = rpl__view_grad(&s, t, 1, 0);
+        const float* db = rpl__view_data(&s, b, 1, 0);
+        float* da = rpl__view_grad(&s, a, 1, 1);
+        if (!s.err)
+            s.err = !rpl__ok(rplhip_sgemm(0, !b_trans, M, K, N, 1.0f, dt, N, db, b_trans ? K : N, 1.0f, da, K, NULL),
+                             "backward_matmul (dA)");
+        rpl__stage_finish(&s);
+        if (a->backward_fn) a->backward_fn(a);
+    }
+    if (b->grad) {
+        RplStage s = {0};
+        const float* dt = rpl__view_grad(&s, t, 1, 0);
+        const float* da = rpl__view_data(&s, a, 1, 0);
+        float* dbg = rpl__view_grad(&s, b, 1, 1);
+        int st = RPLHIP_OK;
+        if (!s.err) {
+            if (b_trans) /* dB[N,K] += dt^T[N,M] * A[M,K] */
+                st = rplhip_sgemm(1, 0, N, K, M, 1.0f, dt, N, da, K, 1.0f, dbg, K, NULL);
+            else /* dB[K,N] += A^T[K,M] * dt[M,N] */
+                st = rplhip_sgemm(1, 0, K, N, M, 1.0f, da, K, dt, N, 1.0f, dbg, N, NULL);
+            s.err = !rpl__ok(st, "backward_matmul (dB)");
+        }
+        rpl__stage_finish(&s);
+        if (b->backward_fn) b->backward_fn(b);
+    }
+}
+
+/* src/rpl_core.c:418-424 */
+void backward_relu(Tensor* t) {
+    Tensor* a = t->parent1;
+    if (a && a->grad) {
+        RplStage s = {0};
+        const float* dx = rpl__view_data(&s, a, 1, 0);
+        const float* dy = rpl__view_grad(&s, t, 1, 0);
+        float* dg = rpl__view_grad(&s, a, 1, 1);
+        if (!s.err) s.err = !rpl__ok(rplhip_relu_backward(dx, dy, dg, t->size, NULL), "backward_relu");
+        rpl__stage_finish(&s);
+        if (a->backward_fn) a->backward_fn(a);
+    }
+}
+
+/* src/rpl_core.c:437-447 */
+void backward_mse(Tensor* t) {
+    Tensor* pred = t->parent1;
+    Tensor* target = t->parent2;
+    if (pred && pred->grad) {
+        RplStage s = {0};
+        const float* dp = rpl__view_data(&s, pred, 1, 0);
+        const float* dtg = rpl__view_data(&s, target, 1, 0);
+        const float* g0 = rpl__view_grad(&s, t, 1, 0);
+        float* dg = rpl__view_grad(&s, pred, 1, 1);
+        if (!s.err)
+            s.err = !rpl__ok(rplhip_mse_backward(dp, dtg, pred->size, g0, dg, NULL), "backward_mse");
+        rpl__stage_finish(&s);
+        if (pred->backward_fn) pred->backward_fn(pred);
+    }
+}
+
+/* src/rpl_core.c:467-476 */
+void tensor_backward(Tensor* t) {
+    if (!t->requires_grad) return;
+    if (!t->grad) {
+        t->grad = (float*)rpitorch_aligned_alloc(64, (size_t)t->size * sizeof(float));
+        if (!t->grad) return;
+    }
+    for (uint32_t i = 0; i < t->size; i++) t->grad[i] = 1.0f;
+    if (rpl__is_gpu(t)) {
+        if (!rpl__attach_grad(t)) return;
+        if (!rpl__ok(rplhip_fill(rpl__dev_grad(t), t->size, 1.0f, NULL), "tensor_backward")) return;
+    }
+    if (t->backward_fn) t->backward_fn(t);
+}
+
+/* src/rpl_core.c:478-480 */
+void tensor_zero_grad(Tensor* t) {
+    if (!t || !t->grad) return;
+    memset(t->grad, 0, (size_t)t->size * sizeof(float));
+    float* g = rpl__dev_grad(t);
+    if (g) rpl__ok(rplhip_memset(g, 0, (size_t)t->size * sizeof(float), NULL), "tensor_zero_grad");
+}
+
+/* src/rpl_nn.c:23-43: same Xavier-style init from rand(), so a given
+ * srand() seed yields the reference's weights. */
+Linear* linear_create(uint32_t in_features, uint32_t out_features) {
+    Linear* layer = (Linear*)calloc(1, sizeof(Linear));
+    if (!layer) return NULL;
+    layer->in_features = in_features;
+    layer->out_features = out_features;
+    uint32_t weight_shape[2] = {out_features, in_features};
+    layer->weight = tensor_create(2, weight_shape, true);
+    uint32_t bias_shape[1] = {out_features};
+    layer->bias = tensor_create(1, bias_shape, true);
+    float std = sqrtf(2.0f / (in_features + out_features));
+    for (uint32_t i = 0; i < layer->weight->size; i++)
+        layer->weight->data[i] = ((float)rand() / RAND_MAX - 0.5f) * 2.0f * std;
+    for (uint32_t i = 0; i < layer->bias->size; i++) layer->bias->data[i] = 0.0f;
+    return layer;
+}
+
+/* src/rpl_nn.c:55-77: NT GEMM x * W^T into a zeroed buffer, then the
+ * broadcast bias add; matmul_out stays alive as part of the graph. */
+Tensor* linear_forward(Linear* layer, const Tensor* input) {
+    uint32_t output_shape[2] = {input->shape[0], layer->out_features};
+    Tensor* matmul_out = tensor_create(2, output_shape, input->requires_grad || layer->weight->requires_grad);
+    if (!matmul_out) return NULL;
+    int gpu = any_gpu(input, layer->weight) || rpl__is_gpu(layer->bias);
+    if (gpu && !rpl__attach(matmul_out, 0)) return NULL;
+    tensor_fill(matmul_out, 0.0f);
+    tensor_gemm(matmul_out, input, layer->weight, 1.0f, 0.0f, false, true);
+    if (matmul_out->requires_grad) {
+        matmul_out->parent1 = (Tensor*)input;
+        matmul_out->parent2 = layer->weight;
+        matmul_out->backward_fn = backward_matmul;
+        matmul_out->is_leaf = false;
+    }
+    Tensor* out = tensor_create(2, output_shape, matmul_out->requires_grad || layer->bias->requires_grad);
+    if (!out) return NULL;
+    if (gpu && !rpl__attach(out, 0)) return NULL;
+    tensor_add_out(out, matmul_out, layer->bias);
+    return out;
+}
+
+/* src/rpl_nn.c:79-83 */
+void linear_free(Linear* layer) {
+    if (!layer) return;
+    tensor_free(layer->weight);
+    tensor_free(layer->bias);
+    free(layer);
+}

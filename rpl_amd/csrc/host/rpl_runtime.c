@@ -1,0 +1,379 @@
+/*
+ * Tensor memory, the device-buffer registry behind Tensor.gpu_buffer, the
+ * staging of host tensors, and the device seam of include/rpl.h
+ * (rpl_gpu_init / tensor_to_gpu / tensor_from_gpu, src/rpl_gpu.c:88-230).
+ */
+#define _GNU_SOURCE
+#include <pthread.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "rpl_host.h"
+
+/* ------------------------------------------------------------ errors */
+
+static __thread char g_last_error[512];
+
+const char* rpl_last_error(void) { return g_last_error; }
+
+int rpl__ok(int st, const char* what) {
+    if (st == RPLHIP_OK) return 1;
+    snprintf(g_last_error, sizeof(g_last_error), "%s: %s", what, rplhip_last_error());
+    fprintf(stderr, "rpl: %s\n", g_last_error);
+    return 0;
+}
+
+int rpl__bad(const char* what, const char* fmt, ...) {
+    char msg[400];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof(msg), fmt, ap);
+    va_end(ap);
+    snprintf(g_last_error, sizeof(g_last_error), "%s: %s", what, msg);
+    fprintf(stderr, "rpl: %s\n", g_last_error);
+    return 0;
+}
+
+/* ------------------------------------------------------- device pool */
+
+typedef struct {
+    void* p;
+    size_t bytes;
+} PoolBlock;
+
+static pthread_mutex_t g_pool_mu = PTHREAD_MUTEX_INITIALIZER;
+static PoolBlock* g_pool;
+static size_t g_pool_len, g_pool_cap;
+
+static size_t pool_round(size_t b) { return (b + 255) & ~(size_t)255; }
+
+void* rpl__pool_alloc(size_t bytes) {
+    if (bytes == 0) bytes = 1;
+    bytes = pool_round(bytes);
+    pthread_mutex_lock(&g_pool_mu);
+    for (size_t i = 0; i < g_pool_len; i++) {
+        if (g_pool[i].bytes == bytes) {
+            void* p = g_pool[i].p;
+            g_pool[i] = g_pool[--g_pool_len];
+            pthread_mutex_unlock(&g_pool_mu);
+            return p;
+        }
+    }
+    pthread_mutex_unlock(&g_pool_mu);
+    void* p = NULL;
+    if (rplhip_malloc(&p, bytes) != RPLHIP_OK) {
+        /* Release cached blocks and retry once. */
+        rplhip_synchronize();
+        rpl__pool_release_all();
+        if (!rpl__ok(rplhip_malloc(&p, bytes), "device allocation")) return NULL;
+    }
+    return p;
+}
+
+void rpl__pool_free(void* p, size_t bytes) {
+    if (!p) return;
+    bytes = pool_round(bytes ? bytes : 1);
+    pthread_mutex_lock(&g_pool_mu);
+    if (g_pool_len == g_pool_cap) {
+        size_t nc = g_pool_cap ? 2 * g_pool_cap : 64;
+        PoolBlock* nb = (PoolBlock*)realloc(g_pool, nc * sizeof(PoolBlock));
+        if (!nb) {
+            pthread_mutex_unlock(&g_pool_mu);
+            rplhip_free(p);
+            return;
+        }
+        g_pool = nb;
+        g_pool_cap = nc;
+    }
+    g_pool[g_pool_len].p = p;
+    g_pool[g_pool_len].bytes = bytes;
+    g_pool_len++;
+    pthread_mutex_unlock(&g_pool_mu);
+}
+
+void rpl__pool_release_all(void) {
+    pthread_mutex_lock(&g_pool_mu);
+    for (size_t i = 0; i < g_pool_len; i++) rplhip_free(g_pool[i].p);
+    g_pool_len = 0;
+    pthread_mutex_unlock(&g_pool_mu);
+}
+
+/* ------------------------------------------------ device-buffer registry */
+
+typedef struct {
+    float* data;
+    float* grad;
+    size_t bytes;
+    int used;
+} RegEntry;
+
+static pthread_mutex_t g_reg_mu = PTHREAD_MUTEX_INITIALIZER;
+static RegEntry* g_reg;
+static uint32_t g_reg_len, g_reg_cap;
+
+static RegEntry* reg_get(uint32_t h) {
+    RegEntry* e = NULL;
+    pthread_mutex_lock(&g_reg_mu);
+    if (h >= 1 && h <= g_reg_len && g_reg[h - 1].used) e = &g_reg[h - 1];
+    pthread_mutex_unlock(&g_reg_mu);
+    return e;
+}
+
+static uint32_t reg_new(float* data, float* grad, size_t bytes) {
+    pthread_mutex_lock(&g_reg_mu);
+    uint32_t h = 0;
+    for (uint32_t i = 0; i < g_reg_len; i++)
+        if (!g_reg[i].used) {
+            h = i + 1;
+            break;
+        }
+    if (!h) {
+        if (g_reg_len == g_reg_cap) {
+            uint32_t nc = g_reg_cap ? 2 * g_reg_cap : 256;
+            RegEntry* nr = (RegEntry*)realloc(g_reg, nc * sizeof(RegEntry));
+            if (!nr) {
+                pthread_mutex_unlock(&g_reg_mu);
+                return 0;
+            }
+            g_reg = nr;
+            g_reg_cap = nc;
+        }
+        h = ++g_reg_len;
+    }
+    g_reg[h - 1].data = data;
+    g_reg[h - 1].grad = grad;
+    g_reg[h - 1].bytes = bytes;
+    g_reg[h - 1].used = 1;
+    pthread_mutex_unlock(&g_reg_mu);
+    return h;
+}
+
+static void reg_release(uint32_t h) {
+    RegEntry* e = reg_get(h);
+    if (!e) return;
+    rpl__pool_free(e->data, e->bytes);
+    if (e->grad) rpl__pool_free(e->grad, e->bytes);
+    pthread_mutex_lock(&g_reg_mu);
+    e->used = 0;
+    e->data = e->grad = NULL;
+    pthread_mutex_unlock(&g_reg_mu);
+}
+
+int rpl__is_gpu(const Tensor* t) { return t && t->device == DEVICE_GPU && reg_get(t->gpu_buffer) != NULL; }
+
+float* rpl__dev_data(const Tensor* t) {
+    RegEntry* e = (t && t->device == DEVICE_GPU) ? reg_get(t->gpu_buffer) : NULL;
+    return e ? e->data : NULL;
+}
+
+float* rpl__dev_grad(const Tensor* t) {
+    RegEntry* e = (t && t->device == DEVICE_GPU) ? reg_get(t->gpu_buffer) : NULL;
+    return e ? e->grad : NULL;
+}
+
+int rpl__attach(Tensor* t, int upload) {
+    if (rpl__is_gpu(t)) return 1;
+    size_t bytes = (size_t)t->size * sizeof(float);
+    float* d = (float*)rpl__pool_alloc(bytes);
+    if (!d) return 0;
+    float* g = NULL;
+    if (t->grad) {
+        g = (float*)rpl__pool_alloc(bytes);
+        if (!g || !rpl__ok(upload ? rplhip_memcpy_htod(g, t->grad, bytes)
+                                  : rplhip_memset(g, 0, bytes, NULL),
+                           "tensor grad to device")) {
+            rpl__pool_free(d, bytes);
+            if (g) rpl__pool_free(g, bytes);
+            return 0;
+        }
+    }
+    if (upload && !rpl__ok(rplhip_memcpy_htod(d, t->data, bytes), "tensor to device")) {
+        rpl__pool_free(d, bytes);
+        if (g) rpl__pool_free(g, bytes);
+        return 0;
+    }
+    uint32_t h = reg_new(d, g, bytes);
+    if (!h) {
+        rpl__pool_free(d, bytes);
+        if (g) rpl__pool_free(g, bytes);
+        return rpl__bad("tensor_to_gpu", "registry allocation failed");
+    }
+    t->gpu_buffer = h;
+    t->device = DEVICE_GPU;
+    return 1;
+}
+
+int rpl__attach_grad(Tensor* t) {
+    RegEntry* e = (t && t->device == DEVICE_GPU) ? reg_get(t->gpu_buffer) : NULL;
+    if (!e) return 0;
+    if (e->grad) return 1;
+    float* g = (float*)rpl__pool_alloc(e->bytes);
+    if (!g) return 0;
+    if (!rpl__ok(rplhip_memset(g, 0, e->bytes, NULL), "device gradient")) {
+        rpl__pool_free(g, e->bytes);
+        return 0;
+    }
+    pthread_mutex_lock(&g_reg_mu);
+    e->grad = g;
+    pthread_mutex_unlock(&g_reg_mu);
+    return 1;
+}
+
+/* ---------------------------------------------------------------- staging */
+
+void* rpl__stage_host(RplStage* s, void* host, size_t bytes, int upload, int writeback) {
+    if (s->err) return NULL;
+    if (s->n == RPL_STAGE_MAX) {
+        s->err = 1;
+        rpl__bad("staging", "too many staged buffers");
+        return NULL;
+    }
+    void* d = rpl__pool_alloc(bytes);
+    if (!d) {
+        s->err = 1;
+        return NULL;
+    }
+    if (upload && bytes && !rpl__ok(rplhip_memcpy_htod(d, host, bytes), "host to device copy")) {
+        rpl__pool_free(d, bytes);
+        s->err = 1;
+        return NULL;
+    }
+    s->e[s->n].dev = d;
+    s->e[s->n].host = host;
+    s->e[s->n].bytes = bytes;
+    s->e[s->n].writeback = writeback;
+    s->n++;
+    return d;
+}
+
+float* rpl__view_data(RplStage* s, const Tensor* t, int upload, int writeback) {
+    if (s->err) return NULL;
+    float* d = rpl__dev_data(t);
+    if (d) return d;
+    return (float*)rpl__stage_host(s, t->data, (size_t)t->size * sizeof(float), upload, writeback);
+}
+
+float* rpl__view_grad(RplStage* s, const Tensor* t, int upload, int writeback) {
+    if (s->err) return NULL;
+    if (rpl__is_gpu(t)) {
+        float* g = rpl__dev_grad(t);
+        if (!g) {
+            s->err = 1;
+            rpl__bad("autograd", "GPU tensor has no device gradient");
+        }
+        return g;
+    }
+    return (float*)rpl__stage_host(s, t->grad, (size_t)t->size * sizeof(float), upload, writeback);
+}
+
+int rpl__stage_finish(RplStage* s) {
+    int ok = !s->err;
+    int any_wb = 0;
+    for (int i = 0; i < s->n; i++) any_wb |= s->e[i].writeback;
+    if (ok && any_wb) {
+        for (int i = 0; i < s->n && ok; i++)
+            if (s->e[i].writeback && s->e[i].bytes)
+                ok = rpl__ok(rplhip_memcpy_dtoh(s->e[i].host, s->e[i].dev, s->e[i].bytes), "device to host copy");
+    }
+    for (int i = 0; i < s->n; i++) rpl__pool_free(s->e[i].dev, s->e[i].bytes);
+    s->n = 0;
+    return ok;
+}
+
+/* ----------------------------------------------------------- Tensor memory */
+
+/* src/rpl_core.c:33-41 */
+void* rpitorch_aligned_alloc(size_t alignment, size_t size) {
+    void* p = NULL;
+    if (posix_memalign(&p, alignment, size ? size : 1) != 0) return NULL;
+    return p;
+}
+
+void rpitorch_aligned_free(void* ptr) { free(ptr); }
+
+/* src/rpl_core.c:43-70 */
+Tensor* tensor_create(uint32_t dims, const uint32_t* shape, bool requires_grad) {
+    Tensor* t = (Tensor*)calloc(1, sizeof(Tensor));
+    if (!t) return NULL;
+    if (dims > MAX_DIMS) {
+        free(t);
+        rpl__bad("tensor_create", "dims %u > MAX_DIMS", dims);
+        return NULL;
+    }
+    t->dims = dims;
+    t->size = 1;
+    for (uint32_t i = 0; i < dims; i++) {
+        t->shape[i] = shape[i];
+        t->size *= shape[i];
+    }
+    if (dims) {
+        t->strides[dims - 1] = 1;
+        for (int i = (int)dims - 2; i >= 0; i--) t->strides[i] = t->strides[i + 1] * t->shape[i + 1];
+    }
+    size_t bytes = (size_t)t->size * sizeof(float);
+    t->_allocation = rpitorch_aligned_alloc(64, bytes);
+    t->_alloc_size = bytes;
+    t->data = (float*)t->_allocation;
+    if (requires_grad) {
+        t->grad = (float*)rpitorch_aligned_alloc(64, bytes);
+        if (t->grad) memset(t->grad, 0, bytes);
+    }
+    t->requires_grad = requires_grad;
+    t->is_leaf = true;
+    return t;
+}
+
+/* src/rpl_core.c:72-77, plus the device buffers */
+void tensor_free(Tensor* t) {
+    if (!t) return;
+    if (t->device == DEVICE_GPU && t->gpu_buffer) reg_release(t->gpu_buffer);
+    free(t->_allocation);
+    free(t->grad);
+    free(t);
+}
+
+/* src/rpl_core.c:83-86 (the device copy too when GPU-resident) */
+void tensor_fill(Tensor* t, float value) {
+    if (!t) return;
+    for (uint32_t i = 0; i < t->size; i++) t->data[i] = value;
+    float* d = rpl__dev_data(t);
+    if (d) rpl__ok(rplhip_fill(d, t->size, value, NULL), "tensor_fill");
+}
+
+/* ------------------------------------------------------------ device seam */
+
+bool rpl_gpu_init(void) { return rpl__ok(rplhip_init(), "rpl_gpu_init"); }
+
+void rpl_gpu_shutdown(void) {
+    if (rplhip_init() != RPLHIP_OK) return;
+    rplhip_synchronize();
+    rpl__pool_release_all();
+}
+
+void rpl_gpu_synchronize(void) { rpl__ok(rplhip_synchronize(), "rpl_gpu_synchronize"); }
+
+void* rpl_gpu_stream(void) { return NULL; }
+
+float* rpl_tensor_device_data(const Tensor* t) { return rpl__dev_data(t); }
+float* rpl_tensor_device_grad(const Tensor* t) { return rpl__dev_grad(t); }
+
+/* src/rpl_gpu.c:201-214: upload and mark GPU-resident (no-op if already). */
+void tensor_to_gpu(Tensor* t) {
+    if (!t || rpl__is_gpu(t)) return;
+    if (!rpl_gpu_init()) return;
+    rpl__attach(t, 1);
+}
+
+/* src/rpl_gpu.c:217-230: copy the device values back into t->data (and the
+ * gradient into t->grad); the tensor stays GPU-resident, as in the reference. */
+void tensor_from_gpu(Tensor* t) {
+    if (!t || t->device == DEVICE_CPU) return;
+    float* d = rpl__dev_data(t);
+    if (!d) return;
+    size_t bytes = (size_t)t->size * sizeof(float);
+    if (!rpl__ok(rplhip_memcpy_dtoh(t->data, d, bytes), "tensor_from_gpu")) return;
+    float* g = rpl__dev_grad(t);
+    if (g && t->grad) rpl__ok(rplhip_memcpy_dtoh(t->grad, g, bytes), "tensor_from_gpu (grad)");
+}

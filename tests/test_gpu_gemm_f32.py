@@ -1,0 +1,183 @@
+"""FP32 GEMM on f32 MFMA vs the oracle / reference golden vectors.
+
+Tolerance (written here, as BASELINE.json's north star states it):
+max_ij |C - C_ref| / sum_k |a_ik b_kj| <= 1e-5 * sqrt(K).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import rpl_amd
+from conftest import seed
+from gpu_util import fp32_tol, gemm_err_ratio, say, sgemm
+
+pytestmark = pytest.mark.gpu
+
+
+def op(X, t):
+    return X.T if t else X
+
+
+@pytest.mark.parametrize("name,ta,tb", [("nn", 0, 0), ("nt", 0, 1), ("tn", 1, 0), ("tt", 1, 1)])
+def test_sgemm_golden(gpu, golden, name, ta, tb):
+    A, B, C0 = golden[f"sgemm_{name}_A"], golden[f"sgemm_{name}_B"], golden[f"sgemm_{name}_C0"]
+    M, N = C0.shape
+    K = A.shape[0] if ta else A.shape[1]
+    say("sgemm golden", name, M, N, K)
+    out = sgemm(A, B, C0, M, N, K, 0.75, -0.5, ta, tb)
+    assert gemm_err_ratio(out, op(A, ta), op(B, tb), golden[f"sgemm_{name}_C"], 0.75, -0.5, C0) <= fp32_tol(K)
+
+
+def test_sgemm_nan_in_c_propagates(gpu, golden):
+    say("sgemm nan")
+    out = sgemm(golden["sgemm_nan_A"], golden["sgemm_nan_A"], golden["sgemm_nan_C0"], 4, 4, 4, 1.0, 0.0)
+    ref = golden["sgemm_nan_C"]
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    np.testing.assert_allclose(out[~np.isnan(ref)], ref[~np.isnan(ref)], rtol=1e-6)
+
+
+def test_sgemm_known_answers(gpu):
+    # tests/full_system_check.py:33-37 and examples/gpu_test.c:106-128 (exact)
+    say("sgemm known answers")
+    eye = np.eye(128, dtype=np.float32)
+    ones = np.ones((128, 128), np.float32)
+    assert np.array_equal(sgemm(eye, ones, np.zeros_like(ones), 128, 128, 128), ones)
+    o32 = np.ones((32, 32), np.float32)
+    assert np.array_equal(sgemm(o32, np.eye(32, dtype=np.float32), np.zeros_like(o32), 32, 32, 32), o32)
+    A = np.random.default_rng(1).standard_normal((256, 256)).astype(np.float32)
+    assert np.array_equal(sgemm(A, np.eye(256, dtype=np.float32), np.zeros_like(A), 256, 256, 256), A)
+
+
+SHAPES = [(1, 1, 1), (3, 5, 7), (127, 129, 65), (130, 7, 300), (64, 256, 32), (200, 130, 1), (17, 33, 2049),
+          (256, 256, 0)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_ragged_vs_oracle(gpu, orc, M, N, K, ta, tb):
+    rng = np.random.default_rng(M * 1000 + N * 10 + K + 7 * ta + 3 * tb)
+    A = rng.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (N, K) if tb else (K, N)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+    say("sgemm ragged", M, N, K, ta, tb)
+    out = sgemm(A, B, C0, M, N, K, 1.25, 0.5, ta, tb)
+    ref = orc.sgemm(A, B, C0, M, N, K, 1.25, 0.5, bool(ta), bool(tb))
+    assert gemm_err_ratio(out, op(A, ta), op(B, tb), ref, 1.25, 0.5, C0) <= fp32_tol(K)
+
+
+def test_sgemm_leading_dimensions(gpu, orc):
+    # Sub-matrix views: lda/ldb/ldc larger than the extents (gemm_optimized's lda/ldb/ldc).
+    rng = np.random.default_rng(3)
+    M, N, K = 70, 90, 110
+    Abig = rng.uniform(-1, 1, (M, K + 13)).astype(np.float32)
+    Bbig = rng.uniform(-1, 1, (K, N + 6)).astype(np.float32)
+    Cbig = rng.uniform(-1, 1, (M, N + 3)).astype(np.float32)
+    say("sgemm ld")
+    out = sgemm(Abig, Bbig, Cbig, M, N, K, 1.0, 1.0, lda=K + 13, ldb=N + 6, ldc=N + 3)
+    ref = Cbig.copy()
+    ref[:, :N] = orc.sgemm(Abig[:, :K].copy(), Bbig[:, :N].copy(), Cbig[:, :N].copy(), M, N, K, 1.0, 1.0)
+    assert np.array_equal(out[:, N:], Cbig[:, N:])  # untouched padding
+    assert gemm_err_ratio(out[:, :N], Abig[:, :K], Bbig[:, :N], ref[:, :N], 1.0, 1.0, Cbig[:, :N]) <= fp32_tol(K)
+
+
+def test_config0_512_vs_oracle(gpu, orc):
+    n = 512
+    A = rpl_amd.fill_uniform(n * n, seed(0, 0)).reshape(n, n)
+    B = rpl_amd.fill_uniform(n * n, seed(0, 1)).reshape(n, n)
+    say("config 0: sgemm 512^3")
+    out = sgemm(A, B, np.zeros((n, n), np.float32), n, n, n)
+    ref = orc.sgemm(A, B, np.zeros((n, n), np.float32), n, n, n)
+    assert gemm_err_ratio(out, A, B, ref) <= fp32_tol(n)
+
+
+def test_config4_8192_sampled_rows(gpu):
+    n = 8192
+    A = rpl_amd.fill_normal(n * n, seed(4, 0)).reshape(n, n)
+    B = rpl_amd.fill_normal(n * n, seed(4, 1)).reshape(n, n)
+    say("config 4: sgemm 8192^3")
+    out = sgemm(A, B, np.zeros((n, n), np.float32), n, n, n)
+    rows = np.random.default_rng(0).choice(n, 24, replace=False)
+    ref = A[rows].astype(np.float64) @ B.astype(np.float64)
+    denom = np.abs(A[rows].astype(np.float64)) @ np.abs(B.astype(np.float64))
+    assert np.max(np.abs(out[rows] - ref) / denom) <= fp32_tol(n)
+    # Size-independent property over every row: C @ x == A @ (B @ x).
+    x = np.random.default_rng(1).standard_normal(n)
+    lhs = out.astype(np.float64) @ x
+    rhs = A.astype(np.float64) @ (B.astype(np.float64) @ x)
+    scale = np.abs(A.astype(np.float64)) @ (np.abs(B.astype(np.float64)) @ np.abs(x))
+    assert np.max(np.abs(lhs - rhs) / scale) <= fp32_tol(n)
+
+
+# ---------------------------------------------------- through include/rpl.h
+
+def tensor_from(lib, arr, requires_grad=False):
+    arr = np.ascontiguousarray(arr, np.float32)
+    shape = (C.c_uint32 * arr.ndim)(*arr.shape)
+    t = lib.tensor_create(arr.ndim, shape, requires_grad)
+    C.memmove(t.contents.data, arr.ctypes.data, arr.nbytes)
+    return t
+
+
+def tensor_data(t, shape):
+    return np.ctypeslib.as_array(t.contents.data, shape=(t.contents.size,)).copy().reshape(shape)
+
+
+@pytest.mark.parametrize("resident", [False, True])
+def test_tensor_gemm_api(gpu, orc, golden, resident):
+    lib = gpu
+    for name, ta, tb in (("nn", 0, 0), ("nt", 0, 1), ("tn", 1, 0), ("tt", 1, 1)):
+        A, B, C0 = golden[f"sgemm_{name}_A"], golden[f"sgemm_{name}_B"], golden[f"sgemm_{name}_C0"]
+        M, N = C0.shape
+        K = A.shape[0] if ta else A.shape[1]
+        tA, tB, tC = tensor_from(lib, A), tensor_from(lib, B), tensor_from(lib, C0)
+        if resident:
+            for t in (tA, tB, tC):
+                lib.tensor_to_gpu(t)
+            assert tC.contents.device == rpl_amd.DEVICE_GPU and tC.contents.gpu_buffer != 0
+        say("tensor_gemm", name, "resident" if resident else "host")
+        lib.tensor_gemm(tC, tA, tB, 0.75, -0.5, bool(ta), bool(tb))
+        if resident:
+            lib.tensor_from_gpu(tC)
+        out = tensor_data(tC, (M, N))
+        assert gemm_err_ratio(out, op(A, ta), op(B, tb), golden[f"sgemm_{name}_C"], 0.75, -0.5, C0) <= fp32_tol(K)
+        for t in (tA, tB, tC):
+            lib.tensor_free(t)
+
+
+def test_tensor_matmul_and_matmul_gpu(gpu, orc):
+    lib = gpu
+    rng = np.random.default_rng(8)
+    A = rng.standard_normal((100, 60)).astype(np.float32)
+    B = rng.standard_normal((60, 80)).astype(np.float32)
+    tA, tB = tensor_from(lib, A), tensor_from(lib, B)
+    say("tensor_matmul")
+    out = lib.tensor_matmul(tA, tB)
+    ref = orc.sgemm(A, B, np.zeros((100, 80), np.float32), 100, 80, 60)
+    assert gemm_err_ratio(tensor_data(out, (100, 80)), A, B, ref) <= fp32_tol(60)
+    tC = tensor_from(lib, np.zeros((100, 80), np.float32))
+    say("tensor_matmul_gpu")
+    lib.tensor_matmul_gpu(tC, tA, tB)
+    lib.tensor_from_gpu(tC)
+    assert gemm_err_ratio(tensor_data(tC, (100, 80)), A, B, ref) <= fp32_tol(60)
+    for t in (tA, tB, tC, out):
+        lib.tensor_free(t)
+
+
+def test_parallel_gemm_optimized(gpu, orc, golden):
+    lib = gpu
+    fp = C.POINTER(C.c_float)
+    A, B, C0 = golden["gemmopt_A"], golden["gemmopt_B"], golden["gemmopt_C0"].copy()
+    say("parallel_gemm_optimized golden")
+    lib.parallel_gemm_optimized(A.ctypes.data_as(fp), B.ctypes.data_as(fp), C0.ctypes.data_as(fp), 8, 4, 16)
+    assert gemm_err_ratio(C0, A, B, golden["gemmopt_C"], 1.0, 1.0, golden["gemmopt_C0"]) <= fp32_tol(16)
+    rng = np.random.default_rng(4)
+    M, N, K = 300, 257, 513
+    A = rng.uniform(0, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(0, 1, (K, N)).astype(np.float32)
+    C1 = rng.uniform(0, 1, (M, N)).astype(np.float32)
+    out = C1.copy()
+    say("parallel_gemm_optimized random")
+    lib.parallel_gemm_optimized(A.ctypes.data_as(fp), B.ctypes.data_as(fp), out.ctypes.data_as(fp), M, N, K)
+    ref = orc.sgemm(A, B, C1, M, N, K, 1.0, 1.0)
+    assert gemm_err_ratio(out, A, B, ref, 1.0, 1.0, C1) <= fp32_tol(K)

@@ -1,0 +1,205 @@
+"""INT8 GEMMs on i8 MFMA vs the oracle and the reference golden vectors.
+Bar: bit-exact (int32 accumulators, requantized int32, fused fp32 dequant)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import rpl_amd
+from conftest import bits_equal, seed
+from gpu_util import down, empty, gemm_int8, linear_int8, linear_int8_dequant, say, up
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("case", ["zp", "unit", "k1041", "overflow", "sc0", "tiny"])
+def test_gemm_int8_golden(gpu, golden, case):
+    A, B = golden[f"i8_{case}_A"], golden[f"i8_{case}_B"]
+    sa, sb, sc = (float(v) for v in golden[f"i8_{case}_params"])
+    za, zb = (int(v) for v in golden[f"i8_{case}_zp"])
+    M, K = A.shape
+    N = B.shape[1]
+    say("gemm_int8 golden", case, M, N, K)
+    assert bits_equal(gemm_int8(A, B, M, N, K, sa, sb, sc, za, zb), golden[f"i8_{case}_C"])
+
+
+def test_gemm_int8_rpl_api(gpu, golden):
+    # include/rpl.h gemm_int8 on host pointers (staged through the device).
+    i8p, i32p = C.POINTER(C.c_int8), C.POINTER(C.c_int32)
+    A, B = golden["i8_zp_A"], golden["i8_zp_B"]
+    M, K = A.shape
+    N = B.shape[1]
+    out = np.zeros((M, N), np.int32)
+    say("rpl.h gemm_int8")
+    gpu.gemm_int8(A.ctypes.data_as(i8p), B.ctypes.data_as(i8p), out.ctypes.data_as(i32p), M, N, K, 0.01, 0.02, 0.5,
+                  3, -5)
+    assert bits_equal(out, golden["i8_zp_C"])
+
+
+SHAPES = [(1, 1, 1), (4, 9, 16), (16, 100, 64), (17, 31, 300), (129, 127, 129), (256, 256, 512), (64, 8, 1000),
+          (5, 300, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_int8_ragged_vs_oracle(gpu, orc, M, N, K):
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, (K, N), dtype=np.int8)
+    for (sa, sb, sc, za, zb) in ((1.0, 1.0, 1.0, 0, 0), (0.013, 0.7, 0.29, -2, 9)):
+        say("gemm_int8 ragged", M, N, K, za, zb)
+        got = gemm_int8(A, B, M, N, K, sa, sb, sc, za, zb)
+        assert bits_equal(got, orc.gemm_int8(A, B, M, N, K, sa, sb, sc, za, zb))
+
+
+@pytest.mark.parametrize("name", ["bias", "nobias", "m1"])
+def test_linear_int8_golden(gpu, golden, name):
+    x, w = golden[f"lin8_{name}_x"], golden[f"lin8_{name}_w"]
+    bias = golden.get(f"lin8_{name}_bias")
+    M, K = x.shape
+    N = w.shape[0]
+    say("linear_int8 golden", name)
+    assert bits_equal(linear_int8(x, w, bias, M, K, N), golden[f"lin8_{name}_out"])
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 64, 33), (3, 67, 40), (4, 8192, 257), (16, 1000, 64), (17, 512, 129),
+                                   (100, 4096, 96), (300, 48, 512)])
+def test_linear_int8_vs_oracle(gpu, orc, M, K, N):
+    rng = np.random.default_rng(M + K + N)
+    x = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    b = rng.integers(-128, 128, N, dtype=np.int8)
+    say("linear_int8", M, K, N)
+    assert bits_equal(linear_int8(x, w, b, M, K, N), orc.linear_int8(x, w, b, M, K, N))
+    assert bits_equal(linear_int8(x, w, None, M, K, N), orc.linear_int8(x, w, None, M, K, N))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 256, 48), (16, 4096, 130), (77, 320, 200)])
+def test_linear_int8_dequant_vs_oracle(gpu, orc, M, K, N):
+    rng = np.random.default_rng(K)
+    x = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sx = rng.random(M).astype(np.float32) * 0.01
+    sw = rng.random(N).astype(np.float32) * 0.02
+    acc = orc.linear_int8(x, w, None, M, K, N)
+    for xr, wr in ((True, True), (False, False), (True, False)):
+        say("linear_int8_dequant", M, K, N, xr, wr)
+        got = linear_int8_dequant(x, sx if xr else sx[:1], xr, w, sw if wr else sw[:1], wr, M, K, N)
+        assert bits_equal(got, orc.dequant_acc(acc, sx if xr else sx[:1], xr, sw if wr else sw[:1], wr))
+
+
+def test_gemm_int8_dequant_vs_oracle(gpu, orc):
+    lib = gpu
+    rng = np.random.default_rng(31)
+    M, N, K = 70, 90, 200
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, (K, N), dtype=np.int8)
+    sa = np.float32([0.02])
+    sb = rng.random(N).astype(np.float32)
+    dA, dB, dsa, dsb, dY = up(A), up(B), up(sa), up(sb), empty((M, N), np.float32)
+    say("gemm_int8_dequant")
+    rpl_amd.check(lib.rplhip_gemm_int8_dequant(dA.ptr, dsa.ptr, 0, dB.ptr, dsb.ptr, 1, dY.ptr, M, N, K, None))
+    acc = orc.gemm_int8(A, B, M, N, K)
+    assert bits_equal(down(dY, np.float32, (M, N)), orc.dequant_acc(acc, sa, False, sb, True))
+
+
+def test_config1_int8_512(gpu, golden):
+    """Config 1: N(0,1) -> per-tensor symmetric quantize -> int32 GEMM, all on the device."""
+    import hashlib
+
+    lib = gpu
+    n = 512
+    A = rpl_amd.fill_normal(n * n, seed(1, 0))
+    B = rpl_amd.fill_normal(n * n, seed(1, 1))
+    dA, dB = up(A), up(B)
+    qA, qB, sA, sB = empty(n * n, np.int8), empty(n * n, np.int8), empty(1, np.float32), empty(1, np.float32)
+    say("config 1: quantize + gemm_int8 512^3")
+    rpl_amd.check(lib.rplhip_quantize_symmetric(dA.ptr, n * n, qA.ptr, sA.ptr, None))
+    rpl_amd.check(lib.rplhip_quantize_symmetric(dB.ptr, n * n, qB.ptr, sB.ptr, None))
+    acc = empty((n, n), np.int32)
+    rpl_amd.check(lib.rplhip_gemm_int8(qA.ptr, qB.ptr, acc.ptr, n, n, n, 1.0, 1.0, 1.0, 0, 0, None))
+    scales = np.concatenate([down(sA, np.float32, (1,)), down(sB, np.float32, (1,))])
+    assert bits_equal(scales, golden["cfg1_scales"])
+    h = lambda a: hashlib.sha256(a.tobytes()).hexdigest().encode()  # noqa: E731
+    assert h(down(qA, np.int8, (n * n,))) == golden["cfg1_qA_sha"].tobytes()
+    assert h(down(qB, np.int8, (n * n,))) == golden["cfg1_qB_sha"].tobytes()
+    assert h(down(acc, np.int32, (n, n))) == golden["cfg1_acc_sha"].tobytes()
+
+
+@pytest.mark.parametrize("N", [4096, 11008])
+def test_config3_transformer_linear(gpu, orc, N):
+    """Config 3: X [2048,4096] per-token, W [N,4096] per-channel, fused dequant."""
+    lib = gpu
+    M, K = 2048, 4096
+    X = rpl_amd.fill_normal(M * K, seed(3, 0)).reshape(M, K)
+    W = rpl_amd.fill_normal(N * K, seed(3, 1), 0.0, 0.02).reshape(N, K)
+    dX, dW = up(X), up(W)
+    qX, qW = empty((M, K), np.int8), empty((N, K), np.int8)
+    sX, sW = empty(M, np.float32), empty(N, np.float32)
+    say("config 3: per-token / per-channel quantize", N)
+    rpl_amd.check(lib.rplhip_quantize_per_channel(dX.ptr, M, K, qX.ptr, sX.ptr, None))
+    rpl_amd.check(lib.rplhip_quantize_per_channel(dW.ptr, N, K, qW.ptr, sW.ptr, None))
+    qx, sx = down(qX, np.int8, (M, K)), down(sX, np.float32, (M,))
+    qw, sw = down(qW, np.int8, (N, K)), down(sW, np.float32, (N,))
+    oqx, osx = orc.quantize_per_channel(X, M)
+    oqw, osw = orc.quantize_per_channel(W, N)
+    assert bits_equal(qx, oqx) and bits_equal(sx, osx) and bits_equal(qw, oqw) and bits_equal(sw, osw)
+    Y = empty((M, N), np.float32)
+    say("config 3: linear_int8_dequant", M, K, N)
+    rpl_amd.check(lib.rplhip_linear_int8_dequant(qX.ptr, sX.ptr, 1, qW.ptr, sW.ptr, 1, Y.ptr, M, K, N, None))
+    y = down(Y, np.float32, (M, N))
+    rows = np.sort(np.random.default_rng(N).choice(M, 16, replace=False))
+    acc_rows = orc.linear_int8(np.ascontiguousarray(qx[rows]), qw, None, len(rows), K, N)
+    assert bits_equal(y[rows], orc.dequant_acc(acc_rows, sx[rows], True, sw, True))
+    # Every row: the int32 path checked by an exact integer identity.
+    acc = empty((M, N), np.int32)
+    rpl_amd.check(lib.rplhip_linear_int8(qX.ptr, qW.ptr, None, acc.ptr, M, K, N, None))
+    a = down(acc, np.int32, (M, N)).astype(np.int64)
+    assert np.array_equal(a.sum(1), qx.astype(np.int64) @ qw.astype(np.int64).sum(0))
+    assert np.array_equal(a.sum(0), qw.astype(np.int64) @ qx.astype(np.int64).sum(0))
+    assert bits_equal(y, ((a.astype(np.int32).astype(np.float32) * sx[:, None]) * sw[None, :]))
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_config4_skinny(gpu, orc, M):
+    """Config 4 skinny: M in {1,4,16}, K = N = 8192, per-channel W."""
+    lib = gpu
+    K = N = 8192
+    X = rpl_amd.fill_normal(M * K, seed(4, 2)).reshape(M, K)
+    W = rpl_amd.fill_normal(N * K, seed(4, 3)).reshape(N, K)
+    qx, sx = orc.quantize_symmetric(X)
+    qw, sw = orc.quantize_per_channel(W, N)
+    say("config 4 skinny linear_int8", M)
+    got = linear_int8(qx.reshape(M, K), qw, None, M, K, N)
+    ref = orc.linear_int8(qx.reshape(M, K), qw, None, M, K, N)
+    assert bits_equal(got, ref)
+    say("config 4 skinny dequant", M)
+    y = linear_int8_dequant(qx.reshape(M, K), np.float32([sx]), False, qw, sw, True, M, K, N)
+    assert bits_equal(y, orc.dequant_acc(ref, np.float32([sx]), False, sw, True))
+
+
+def test_config4_int8_8192(gpu, orc):
+    """Config 4: 8192^3 per-tensor INT8 (gemm_int8 layout)."""
+    lib = gpu
+    n = 8192
+    A = rpl_amd.fill_normal(n * n, seed(4, 0))
+    B = rpl_amd.fill_normal(n * n, seed(4, 1))
+    dA, dB = up(A), up(B)
+    qA, qB, sA, sB = empty(n * n, np.int8), empty(n * n, np.int8), empty(1, np.float32), empty(1, np.float32)
+    say("config 4: quantize 8192^2 x2")
+    rpl_amd.check(lib.rplhip_quantize_symmetric(dA.ptr, n * n, qA.ptr, sA.ptr, None))
+    rpl_amd.check(lib.rplhip_quantize_symmetric(dB.ptr, n * n, qB.ptr, sB.ptr, None))
+    qa, qb = down(qA, np.int8, (n, n)), down(qB, np.int8, (n, n))
+    oqa, osa = orc.quantize_symmetric(A)
+    assert bits_equal(qa.reshape(-1), oqa) and bits_equal(down(sA, np.float32, (1,)), np.float32([osa]))
+    del dA, dB, A, B
+    acc = empty((n, n), np.int32)
+    say("config 4: gemm_int8 8192^3")
+    rpl_amd.check(lib.rplhip_gemm_int8(qA.ptr, qB.ptr, acc.ptr, n, n, n, 1.0, 1.0, 1.0, 0, 0, None))
+    a = down(acc, np.int32, (n, n))
+    rows = np.sort(np.random.default_rng(5).choice(n, 4, replace=False))
+    ref_rows = orc.gemm_int8(np.ascontiguousarray(qa[rows]), qb, len(rows), n, n)
+    assert bits_equal(a[rows], ref_rows)
+    a64 = a.astype(np.int64)
+    assert np.abs(a64).max() < 2 ** 24  # exact through the float requant with unit scales
+    assert np.array_equal(a64.sum(1), qa.astype(np.int64) @ qb.astype(np.int64).sum(1))
+    assert np.array_equal(a64.sum(0), qb.astype(np.int64).T @ qa.astype(np.int64).sum(0))

@@ -1,0 +1,168 @@
+"""Linear forward/backward and the MLP training step on the device, through
+the reference's own API (linear_create / linear_forward / tensor_relu /
+tensor_mse_loss / tensor_backward) with GPU-resident tensors.
+
+fp32 bar (as BASELINE.json's north star states it): each GEMM-shaped output
+within max |err| / sum|terms| <= 1e-5 * sqrt(K), K its reduction length;
+elementwise outputs within 1e-6 relative."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import rpl_amd
+from conftest import seed
+from gpu_util import down, empty, say, up
+
+pytestmark = pytest.mark.gpu
+
+
+def tensor_from(lib, arr, requires_grad=False):
+    arr = np.ascontiguousarray(arr, np.float32)
+    shape = (C.c_uint32 * arr.ndim)(*arr.shape)
+    t = lib.tensor_create(arr.ndim, shape, requires_grad)
+    C.memmove(t.contents.data, arr.ctypes.data, arr.nbytes)
+    return t
+
+
+def host(t, shape, grad=False):
+    p = t.contents.grad if grad else t.contents.data
+    return np.ctypeslib.as_array(p, shape=(t.contents.size,)).copy().reshape(shape)
+
+
+def run_mlp(lib, X, Y, W1, b1, W2, b2):
+    """One training step through include/rpl.h with everything GPU-resident."""
+    B, IN = X.shape
+    H, O = W1.shape[0], W2.shape[0]
+    l1, l2 = lib.linear_create(IN, H), lib.linear_create(H, O)
+    for layer, W, bb in ((l1, W1, b1), (l2, W2, b2)):
+        C.memmove(layer.contents.weight.contents.data, W.ctypes.data, W.nbytes)
+        C.memmove(layer.contents.bias.contents.data, bb.ctypes.data, bb.nbytes)
+        lib.tensor_to_gpu(layer.contents.weight)
+        lib.tensor_to_gpu(layer.contents.bias)
+    tX, tY = tensor_from(lib, X), tensor_from(lib, Y)
+    lib.tensor_to_gpu(tX)
+    lib.tensor_to_gpu(tY)
+    h = lib.linear_forward(l1, tX)
+    a = lib.tensor_relu(h)
+    o = lib.linear_forward(l2, a)
+    loss = lib.tensor_mse_loss(o, tY)
+    assert all(t.contents.device == rpl_amd.DEVICE_GPU for t in (h, a, o, loss))
+    lib.tensor_backward(loss)
+    for t in (loss, o, h, l1.contents.weight, l1.contents.bias, l2.contents.weight, l2.contents.bias):
+        lib.tensor_from_gpu(t)
+    r = dict(loss=host(loss, (1,))[0], o=host(o, (B, O)), h=host(h, (B, H)),
+             dW1=host(l1.contents.weight, (H, IN), True), db1=host(l1.contents.bias, (H,), True),
+             dW2=host(l2.contents.weight, (O, H), True), db2=host(l2.contents.bias, (O,), True))
+    err = lib.rpl_last_error()
+    assert not err, err
+    return r
+
+
+def check_mlp(r, ref, X, W1, W2, Y):
+    """Compare with the reference values using per-output sum|terms| scales."""
+    X64, W164, W264 = (v.astype(np.float64) for v in (X, W1, W2))
+    B = X.shape[0]
+    h = X64 @ W164.T
+    a = np.maximum(ref["h"].astype(np.float64), 0)
+    scale_o = np.abs(a) @ np.abs(W264.T) + 1e-30
+    tol = lambda K: 1e-5 * np.sqrt(K) * 4  # noqa: E731  (errors compound over two layers)
+    assert np.max(np.abs(r["h"] - ref["h"]) / (np.abs(X64) @ np.abs(W164.T) + 1e-30)) <= tol(X.shape[1])
+    assert np.max(np.abs(r["o"] - ref["o"]) / scale_o) <= tol(W1.shape[0])
+    assert abs(r["loss"] - ref["loss"]) <= 1e-5 * abs(ref["loss"])
+    dO = 2.0 / ref["o"].size * (ref["o"].astype(np.float64) - Y)
+    dA = dO @ W264
+    dH = dA * (ref["h"] > 0)
+    s_dW2 = np.abs(dO.T) @ np.abs(a) + 1e-30
+    s_dW1 = np.abs(dH.T) @ np.abs(X64) + 1e-30
+    assert np.max(np.abs(r["dW2"] - ref["dW2"]) / s_dW2) <= tol(B)
+    assert np.max(np.abs(r["dW1"] - ref["dW1"]) / s_dW1) <= tol(B)
+    assert np.max(np.abs(r["db2"] - ref["db2"]) / (np.abs(dO).sum(0) + 1e-30)) <= tol(B)
+    assert np.max(np.abs(r["db1"] - ref["db1"]) / (np.abs(dH).sum(0) + 1e-30)) <= tol(B)
+    del h
+
+
+def test_mlp_step_golden(gpu, golden, orc):
+    X, Y = golden["mlp_X"], golden["mlp_Y"]
+    W1, b1, W2, b2 = golden["mlp_W1"], golden["mlp_b1"], golden["mlp_W2"], golden["mlp_b2"]
+    say("mlp golden step")
+    r = run_mlp(gpu, X, Y, W1, b1, W2, b2)
+    ref = orc.mlp_step(X, Y, W1, b1, W2, b2)
+    for k in ("o", "dW1", "db1", "dW2", "db2"):  # the oracle reproduces the reference golden bit-exactly
+        assert np.array_equal(ref[k], golden[f"mlp_{k}"])
+    check_mlp(r, ref, X, W1, W2, Y)
+
+
+def test_config2_mlp_step(gpu, orc):
+    """Config 2: MLP 784 -> 128 (ReLU) -> 10, batch 4096, MSE."""
+    B, IN, H, O = 4096, 784, 128, 10
+    X = rpl_amd.fill_uniform(B * IN, seed(2, 0), 0.0, 1.0).reshape(B, IN)
+    _, Y = rpl_amd.fill_labels(B, seed(2, 1), O)
+    W1 = rpl_amd.fill_uniform(H * IN, seed(2, 2), -np.sqrt(6 / IN), np.sqrt(6 / IN)).reshape(H, IN)
+    W2 = rpl_amd.fill_uniform(O * H, seed(2, 3), -np.sqrt(6 / H), np.sqrt(6 / H)).reshape(O, H)
+    b1, b2 = np.zeros(H, np.float32), np.zeros(O, np.float32)
+    say("config 2: mlp step")
+    r = run_mlp(gpu, X, Y, W1, b1, W2, b2)
+    ref = orc.mlp_step(X, Y, W1, b1, W2, b2)
+    check_mlp(r, ref, X, W1, W2, Y)
+
+
+def test_backward_matmul_layout_guess(gpu, golden):
+    lib = gpu
+    tA, tB = tensor_from(lib, golden["bmm_A"], True), tensor_from(lib, golden["bmm_B"], True)
+    lib.tensor_to_gpu(tA)
+    lib.tensor_to_gpu(tB)
+    say("backward_matmul layout guess")
+    out = lib.tensor_matmul(tA, tB)
+    lib.tensor_backward(out)
+    for t in (out, tA, tB):
+        lib.tensor_from_gpu(t)
+    assert np.array_equal(host(out, (2, 2)), golden["bmm_out"])
+    assert np.array_equal(host(tA, (2, 2), True), golden["bmm_dA"])
+    assert np.array_equal(host(tB, (2, 2), True), golden["bmm_dB"])
+
+
+@pytest.mark.parametrize("n,nb", [(4096 * 128, 128), (4096 * 10, 10), (1000, 7), (1003, 7), (64, 64), (5, 1)])
+def test_bias_pieces_vs_oracle(gpu, orc, n, nb):
+    lib = gpu
+    rng = np.random.default_rng(n + nb)
+    mm = rng.standard_normal(n).astype(np.float32)
+    b = rng.standard_normal(nb).astype(np.float32)
+    dmm, db_, dout, dact = up(mm), up(b), empty(n, np.float32), empty(n, np.float32)
+    say("bias_add_relu", n, nb)
+    rpl_amd.check(lib.rplhip_bias_add_relu(dmm.ptr, db_.ptr, dout.ptr, dact.ptr, n, nb, None))
+    out = orc.add_broadcast(mm, b)
+    assert np.array_equal(down(dout, np.float32, (n,)), out)
+    assert np.array_equal(down(dact, np.float32, (n,)), orc.relu(out))
+    g0 = rng.standard_normal(nb).astype(np.float32)
+    dg = up(g0)
+    say("bias_grad", n, nb)
+    rpl_amd.check(lib.rplhip_bias_grad(dmm.ptr, n, dg.ptr, nb, None))
+    _, ref = orc.add_backward(mm, None, g0)
+    scale = np.zeros(nb)
+    np.add.at(scale, np.arange(n) % nb, np.abs(mm))
+    assert np.max(np.abs(down(dg, np.float32, (nb,)) - ref) / (scale + np.abs(g0))) <= 1e-5 * np.sqrt(n / nb + 1)
+    dy = rng.standard_normal(n).astype(np.float32)
+    dx0 = rng.standard_normal(n).astype(np.float32)
+    ddy, ddx = up(dy), up(dx0)
+    say("relu_backward", n)
+    rpl_amd.check(lib.rplhip_relu_backward(dmm.ptr, ddy.ptr, ddx.ptr, n, None))
+    assert np.array_equal(down(ddx, np.float32, (n,)), orc.relu_backward(mm, dy, dx0))
+
+
+def test_mse_vs_oracle(gpu, orc):
+    lib = gpu
+    n = 40960
+    rng = np.random.default_rng(2)
+    p = rng.standard_normal(n).astype(np.float32)
+    t = rng.standard_normal(n).astype(np.float32)
+    dp, dt, dl = up(p), up(t), empty(1, np.float32)
+    say("mse")
+    rpl_amd.check(lib.rplhip_mse_loss(dp.ptr, dt.ptr, n, dl.ptr, None))
+    loss = down(dl, np.float32, (1,))[0]
+    assert abs(loss - orc.mse_loss(p, t)) <= 1e-5 * np.sqrt(n) * loss
+    g0 = up(np.float32([1.0]))
+    d0 = rng.standard_normal(n).astype(np.float32)
+    dd = up(d0)
+    rpl_amd.check(lib.rplhip_mse_backward(dp.ptr, dt.ptr, n, g0.ptr, dd.ptr, None))
+    np.testing.assert_allclose(down(dd, np.float32, (n,)), orc.mse_backward(p, t, 1.0, d0), rtol=1e-6, atol=1e-7)
