@@ -87,7 +87,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--n", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--cpu-rows", type=int, default=64)
+    ap.add_argument("--cpu-rows", type=int, default=512)
+    ap.add_argument("--only", choices=["int8", "int8-kernel", "fp32", "skinny"],
+                    help="run one leg only (for profiling); the JSON line then has nulls for the rest")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -122,16 +124,20 @@ def main():
         check(lib.rplhip_gemm_int8(qA.ptr, qB.ptr, dC.ptr, n, n, n, float(scales[0]), float(scales[1]), 1.0, 0, 0,
                                    stream))
 
-    log("bench: int8 gemm_int8 8192^3")
-    ms_i8, wall_i8 = timer.time(int8_step, args.steps, args.warmup)
-    tops = ops / (ms_i8 * 1e-3) / 1e12
+    want = lambda leg: args.only in (None, leg)  # noqa: E731
+    ms_i8 = wall_i8 = tops = ms_k = kern_tops = ms_f32 = wall_f32 = tflops = float("nan")
+    if want("int8"):
+        log("bench: int8 gemm_int8 8192^3")
+        ms_i8, wall_i8 = timer.time(int8_step, args.steps, args.warmup)
+        tops = ops / (ms_i8 * 1e-3) / 1e12
 
     # Dominant kernel alone: the i8-MFMA GEMM on B already in [N,K] (what
     # gemm_int8 runs after its transpose pass).
     kern = lambda: check(lib.rplhip_linear_int8(qA.ptr, qB.ptr, None, dC.ptr, n, n, n, stream))  # noqa: E731
-    log("bench: int8 GEMM kernel alone")
-    ms_k, _ = timer.time(kern, args.steps, args.warmup)
-    kern_tops = ops / (ms_k * 1e-3) / 1e12
+    if want("int8-kernel") or args.only is None:
+        log("bench: int8 GEMM kernel alone")
+        ms_k, _ = timer.time(kern, args.steps, args.warmup)
+        kern_tops = ops / (ms_k * 1e-3) / 1e12
 
     # ---- FP32 8192^3 NN (tensor_gemm semantics, alpha=1, beta=0)
     dCf = DeviceBuffer(n * n * 4)
@@ -140,14 +146,15 @@ def main():
     def fp32_step():
         check(lib.rplhip_sgemm(0, 0, n, n, n, 1.0, dA.ptr, n, dB.ptr, n, 0.0, dCf.ptr, n, stream))
 
-    log("bench: fp32 sgemm 8192^3")
-    ms_f32, wall_f32 = timer.time(fp32_step, max(args.steps // 2, 3), 2)
-    tflops = ops / (ms_f32 * 1e-3) / 1e12
+    if want("fp32"):
+        log("bench: fp32 sgemm 8192^3")
+        ms_f32, wall_f32 = timer.time(fp32_step, max(args.steps // 2, 3), 2)
+        tflops = ops / (ms_f32 * 1e-3) / 1e12
 
     # ---- skinny INT8 (M in {1,4,16}, K=N=8192, per-channel W): HBM-bound.
     # Rotate 6 distinct 64 MiB weight copies (> 256 MB MALL) across calls.
     skinny = {}
-    if n == 8192:
+    if n == 8192 and want("skinny"):
         K = N = n
         nw = 6
         Ws = [DeviceBuffer(N * K) for _ in range(nw)]
@@ -171,7 +178,7 @@ def main():
         del Ws
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and args.only is None:
         log(f"bench: cpu baseline (oracle, {args.cpu_rows}-row slab)")
         qa = qA.to_array(np.int8, (n, n))
         qb = qB.to_array(np.int8, (n, n))

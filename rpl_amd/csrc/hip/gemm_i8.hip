@@ -3,9 +3,16 @@
 // Core kernel: NT layout (A [M,K] and B [N,K], both k-contiguous), which is
 // what the MFMA operands want: every lane feeds 16 consecutive k bytes of one
 // row.  Block tile BM x BN x BK staged through LDS (double-buffered, rows
-// padded by 16 bytes so the 16 lanes of a ds_read_b128 phase hit distinct
-// banks), 4 waves each owning a (BM/2) x (BN/2) sub-tile of 16x16 MFMA
-// blocks.  Global loads are 128-bit and coalesced along k.
+// padded by 16 bytes so the lanes of a ds_read_b128 phase hit distinct
+// banks); 4 waves (2 x 2), each owning a (BM/2) x (BN/2) sub-tile of 16x16
+// MFMA blocks.  The large configuration (256 x 256, 128 x 128 per wave, the
+// 256 int32 accumulators living in AGPRs) halves the LDS bytes read per MFMA
+// op compared with 64 x 64 wave tiles, which is what bounds this kernel.
+// Global loads are 128-bit and coalesced along k.  Tiles are visited in an
+// XCD-aware grouped order: workgroups are dispatched round-robin over the 8
+// XCDs, so consecutive tile indices are remapped onto one XCD and grouped
+// 8 tile-rows at a time, which keeps the A and B panels the XCD's 32 CUs
+// share resident in that XCD's L2.
 //
 // The epilogue is fused and selected at compile time:
 //   kRaw     : out = acc + bias[n]                      (linear_int8)
@@ -16,14 +23,28 @@
 // gemm_int8's B is [K,N] (n-contiguous); it is first transposed into a
 // stream-ordered workspace so the NT core serves both layouts.
 //
-// M <= 16 (decode-style skinny GEMMs) runs a separate bandwidth kernel: one
-// block per 16 rows of B, waves split K, each lane streams 16-byte chunks of
-// B straight from HBM into MFMA operands, partial tiles reduced through LDS.
+// M <= 16 (decode-style skinny GEMMs) runs a separate bandwidth kernel: 16
+// waves per block split K, each lane streams 16-byte chunks of B straight
+// from HBM into MFMA operands (A, padded to 16 rows, is the other operand and
+// is reused across the block's two 16-row B panels), and the 16 partial
+// tiles are reduced through LDS before the epilogue.
 #include <math.h>
+#include <stdlib.h>
+
+#include <type_traits>
 
 #include "common.h"
 
 namespace {
+
+// Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 at compile time.
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
 
 enum Epi { kRaw = 0, kRequant = 1, kDequant = 2 };
 
@@ -65,17 +86,7 @@ __device__ __forceinline__ void epilogue_store(const EpiParams& p, uint32_t m, u
     }
 }
 
-// ------------------------------------------------------------ NT core GEMM
-
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int kPitch = BK + 16;  // bytes per LDS row
-constexpr int kWaves = 4, kThreads = 64 * kWaves;
-constexpr int TM = BM / 2, TN = BN / 2;  // wave tile
-constexpr int FM = TM / 16, FN = TN / 16;
-constexpr int kChunksA = BM * BK / 16 / kThreads;  // 16-byte chunks per thread
-constexpr int kChunksB = BN * BK / 16 / kThreads;
-
-// Load one 16-byte chunk (row r, byte column kc) of a k-contiguous tile with
+// Load one 16-byte chunk (row r, byte column k) of a k-contiguous matrix with
 // zero fill outside [rows, K).  ALIGNED: K, ld multiple of 16, base 16-aligned.
 template <bool ALIGNED>
 __device__ __forceinline__ v4i load_chunk(const int8_t* __restrict__ base, uint32_t ld, uint32_t rows,
@@ -97,140 +108,370 @@ __device__ __forceinline__ v4i load_chunk(const int8_t* __restrict__ base, uint3
     }
 }
 
-template <int EPI, bool ALIGNED>
-__global__ void __launch_bounds__(kThreads) k_gemm_i8_nt(const int8_t* __restrict__ A, uint32_t lda,
-                                                         const int8_t* __restrict__ B, uint32_t ldb,
-                                                         uint32_t M, uint32_t N, uint32_t K, EpiParams p) {
-    __shared__ __attribute__((aligned(16))) int8_t As[2][BM * kPitch];
-    __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN * kPitch];
+// Tile index -> (tile_m, tile_n) for a 1-D grid of tm x tn tiles:
+// 1. undo the round-robin XCD dispatch (block b runs on XCD b % 8) so that
+//    each XCD owns a contiguous range of virtual tile indices;
+// 2. walk that range in groups of kGroupM tile-rows, column by column.
+constexpr uint32_t kXcds = 8, kGroupM = 8;
+
+__device__ __forceinline__ void tile_of(uint32_t b, uint32_t tm, uint32_t tn, uint32_t& im, uint32_t& in) {
+    const uint32_t T = tm * tn;
+    const uint32_t q = T / kXcds, r = T % kXcds;
+    const uint32_t x = b % kXcds, idx = b / kXcds;
+    const uint32_t t = x * q + (x < r ? x : r) + idx;
+    const uint32_t group = kGroupM * tn;
+    const uint32_t g = t / group, first = g * kGroupM;
+    const uint32_t gm = tm - first < kGroupM ? tm - first : kGroupM;
+    const uint32_t w = t - g * group;
+    im = first + w % gm;
+    in = w / gm;
+}
+
+// ------------------------------------------------------------ NT core GEMM
+
+// MFMA: v_mfma_i32_32x32x32_i8 (65536 ops, 32 cycles).  It sustains ~95% of
+// the i8 peak from one wave per SIMD, where 16x16x64 with the same number of
+// accumulator registers stalls near 60% (measured on MI355X).  Operand
+// layout: lane l feeds row (or column) l%32 of the 32x32 block with the 16
+// k-bytes 16*(l/32) .. +16 of the 32-k step; the int32 result element r of
+// lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+//
+// Pipeline: three LDS stages, two fragment register sets and two register
+// sets of in-flight HBM loads.  In iteration kt the MFMAs consume tile kt
+// from registers, while the same wave reads tile kt+1's fragments out of
+// LDS, writes tile kt+2 (fetched two iterations earlier) into LDS, and
+// issues the HBM loads of tile kt+4; one barrier per iteration.  LDS latency
+// is hidden behind 32 MFMAs and HBM/L2 latency behind two iterations.  The
+// steady-state iterations carry no conditions (edge tiles and the last
+// iterations run a separate, checked copy of the loop), which lets the
+// compiler wait only for the loads it needs (vmcnt) instead of draining.
+//
+// LDS rows are unpadded 64-byte k-slices; the four 16-byte chunks of row r
+// are stored XOR-swizzled (chunk c at slot c ^ swz(r)), so both the 128-bit
+// fragment reads (16 consecutive rows, same chunk) and the 128-bit tile
+// writes (4 chunks of consecutive rows) touch distinct banks whether the
+// LDS serves 8 lanes x 16 bytes over 32 banks or 16 lanes over 64 banks.
+__device__ __forceinline__ uint32_t swz(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+// Word 3 of a raw buffer resource on gfx950 (32-bit data format, no
+// swizzle, range-checked against num_records).
+constexpr int kBufferFlags = 0x00020000;
+
+template <int BM_, int BN_>
+struct Cfg {
+    static constexpr int BM = BM_, BN = BN_, BK = 64;
+    static constexpr int kThreads = 256;            // 4 waves, 2 x 2
+    static constexpr int TM = BM / 2, TN = BN / 2;  // wave tile
+    static constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 MFMA blocks per wave tile
+    static constexpr int kPitch = BK;  // LDS row pitch in bytes (swizzled, unpadded)
+    static constexpr int kChunksA = BM * BK / 16 / kThreads;
+    static constexpr int kChunksB = BN * BK / 16 / kThreads;
+    static constexpr int kCPR = BK / 16;  // 16-byte chunks per tile row
+    static constexpr int kStages = 4;
+    static constexpr int kStageBytes = (BM + BN) * kPitch;
+    // Epilogue staging: one 32 x TN int32 block-row per wave, padded so
+    // that rows 4 apart (the two lane halves of a store) use disjoint banks.
+    static constexpr int kEpiPitch = TN + 8;
+    static_assert(4 * 32 * kEpiPitch * 4 <= kStages * kStageBytes, "epilogue staging must fit the LDS stages");
+};
+
+using CfgBig = Cfg<256, 256>;
+using CfgSmall = Cfg<128, 128>;
+
+// Fragments of one 32-k step.
+template <class G>
+struct Frags {
+    v4i a[G::FM], b[G::FN];
+};
+
+// Fused epilogue on 4 consecutive columns n..n+3 of row m.
+template <int EPI>
+__device__ __forceinline__ void epilogue_store4(const EpiParams& p, uint32_t m, uint32_t n, uint32_t N, v4i v) {
+    const uint64_t o = (uint64_t)m * p.ldc + n;
+    const bool vec = n + 3 < N && (p.ldc & 3) == 0;
+    if (EPI == kDequant) {
+        const float s = p.sx[p.sx_per_row ? m : 0];
+        float4 y;
+        y.x = (float)v[0] * s * p.sw[p.sw_per_col ? n + 0 : 0];
+        y.y = (float)v[1] * s * p.sw[p.sw_per_col ? n + 1 : 0];
+        y.z = (float)v[2] * s * p.sw[p.sw_per_col ? n + 2 : 0];
+        y.w = (float)v[3] * s * p.sw[p.sw_per_col ? n + 3 : 0];
+        if (vec && (((uintptr_t)p.out_f32) & 15) == 0) {
+            *reinterpret_cast<float4*>(p.out_f32 + o) = y;
+        } else {
+            if (n + 0 < N) p.out_f32[o + 0] = y.x;
+            if (n + 1 < N) p.out_f32[o + 1] = y.y;
+            if (n + 2 < N) p.out_f32[o + 2] = y.z;
+            if (n + 3 < N) p.out_f32[o + 3] = y.w;
+        }
+    } else if (vec && (((uintptr_t)p.out_i32) & 15) == 0) {
+        v4i r;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            int32_t x = v[e];
+            if (EPI == kRaw) {
+                if (p.bias) x = wrap_add(x, (int32_t)p.bias[n + e]);
+            } else {
+                if (p.rowsum_a) x = wrap_add(x, -wrap_mul(p.zb, p.rowsum_a[m]));
+                if (p.rowsum_b) x = wrap_add(x, -wrap_mul(p.za, p.rowsum_b[n + e]));
+                x = wrap_add(x, p.kzz);
+                float result = (float)x * p.sa * p.sb / p.sc;  // ops_extended.c:119
+                x = x86_cvt_i32(roundf(result));
+            }
+            r[e] = x;
+        }
+        *reinterpret_cast<v4i*>(p.out_i32 + o) = r;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (n + e < N) epilogue_store<EPI>(p, m, n + e, v[e]);
+    }
+}
+
+template <class G, int EPI, bool ALIGNED>
+__global__ void __launch_bounds__(256, 1) k_gemm_i8_nt(const int8_t* __restrict__ A, uint32_t lda,
+                                                       const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
+                                                       uint32_t N, uint32_t K, EpiParams p) {
+    constexpr int BM = G::BM, BN = G::BN, BK = G::BK, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
+    constexpr int P = G::kPitch, CPR = G::kCPR, S = G::kStages;
+    __shared__ __attribute__((aligned(16))) int8_t smem[S * G::kStageBytes];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % 64, wave = tid / 64;
     const uint32_t wm = wave / 2, wn = wave % 2;
-    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    uint32_t im, in;
+    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, im, in);
+    const uint32_t m0 = im * BM, n0 = in * BN;
 
-    v4i acc[FM][FN];
+    v16i acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] = (v4i){0, 0, 0, 0};
+        for (int j = 0; j < FN; j++) acc[i][j] = (v16i){};
 
-    v4i ra[kChunksA], rb[kChunksB];
-    auto gload = [&](uint32_t k0) {
+    struct Ld {
+        v4i a[G::kChunksA], b[G::kChunksB];
+    };
+    // HBM -> registers for one k-tile.  The fast path uses raw buffer loads:
+    // one resource per operand based at the tile's first row and sized to
+    // the rows that exist, so rows past M / N read as zeros in hardware; the
+    // lane's byte offset is one VGPR and the chunk / k offsets are scalars.
+    // It needs K % 64 == 0 and operands under 2 GiB; anything else takes
+    // the guarded element path.
+    const uint32_t voff_a = (tid / CPR) * lda + (tid % CPR) * 16;
+    const uint32_t voff_b = (tid / CPR) * ldb + (tid % CPR) * 16;
+    constexpr uint32_t kRowsPerLoad = G::kThreads / CPR;
+    const __amdgpu_buffer_rsrc_t rsrc_a =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(A + (uint64_t)m0 * lda), (short)0,
+                                          (int)((M > m0 ? M - m0 : 0) * lda), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rsrc_b =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(B + (uint64_t)n0 * ldb), (short)0,
+                                          (int)((N > n0 ? N - n0 : 0) * ldb), kBufferFlags);
+    auto gload_fast = [&](uint32_t k0, Ld& g) {
 #pragma unroll
-        for (int i = 0; i < kChunksA; i++) {
-            uint32_t c = tid + i * kThreads;
-            uint32_t r = c / (BK / 16), kc = (c % (BK / 16)) * 16;
-            ra[i] = load_chunk<ALIGNED>(A, lda, M, K, m0 + r, k0 + kc);
+        for (int i = 0; i < G::kChunksA; i++)
+            g.a[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a, k0 + i * kRowsPerLoad * lda, 0);
+#pragma unroll
+        for (int i = 0; i < G::kChunksB; i++)
+            g.b[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b, k0 + i * kRowsPerLoad * ldb, 0);
+    };
+    auto gload_edge = [&](uint32_t k0, Ld& g) {
+#pragma unroll
+        for (int i = 0; i < G::kChunksA; i++) {
+            uint32_t c = tid + i * G::kThreads;
+            g.a[i] = load_chunk<ALIGNED>(A, lda, M, K, m0 + c / CPR, k0 + (c % CPR) * 16);
         }
 #pragma unroll
-        for (int i = 0; i < kChunksB; i++) {
-            uint32_t c = tid + i * kThreads;
-            uint32_t r = c / (BK / 16), kc = (c % (BK / 16)) * 16;
-            rb[i] = load_chunk<ALIGNED>(B, ldb, N, K, n0 + r, k0 + kc);
+        for (int i = 0; i < G::kChunksB; i++) {
+            uint32_t c = tid + i * G::kThreads;
+            g.b[i] = load_chunk<ALIGNED>(B, ldb, N, K, n0 + c / CPR, k0 + (c % CPR) * 16);
         }
     };
-    auto sstore = [&](int buf) {
+    auto sstore = [&](uint32_t stage, const Ld& g) {
+        int8_t* As = smem + stage * G::kStageBytes;
+        int8_t* Bs = As + BM * P;
 #pragma unroll
-        for (int i = 0; i < kChunksA; i++) {
-            uint32_t c = tid + i * kThreads;
-            uint32_t r = c / (BK / 16), kc = (c % (BK / 16)) * 16;
-            *reinterpret_cast<v4i*>(&As[buf][r * kPitch + kc]) = ra[i];
+        for (int i = 0; i < G::kChunksA; i++) {
+            uint32_t c = tid + i * G::kThreads, r = c / CPR;
+            *reinterpret_cast<v4i*>(&As[r * P + ((c % CPR) ^ swz(r)) * 16]) = g.a[i];
         }
 #pragma unroll
-        for (int i = 0; i < kChunksB; i++) {
-            uint32_t c = tid + i * kThreads;
-            uint32_t r = c / (BK / 16), kc = (c % (BK / 16)) * 16;
-            *reinterpret_cast<v4i*>(&Bs[buf][r * kPitch + kc]) = rb[i];
+        for (int i = 0; i < G::kChunksB; i++) {
+            uint32_t c = tid + i * G::kThreads, r = c / CPR;
+            *reinterpret_cast<v4i*>(&Bs[r * P + ((c % CPR) ^ swz(r)) * 16]) = g.b[i];
         }
+    };
+    // MFMA operand fragments of 32-k step kk of the tile in `stage`: lane
+    // feeds row lane%32 of each 32-row block with 16-byte chunk
+    // 2*kk + lane/32.
+    auto fload = [&](uint32_t stage, int kk, Frags<G>& f) {
+        const int8_t* As = smem + stage * G::kStageBytes;
+        const int8_t* Bs = As + BM * P;
+        const uint32_t ch = 2 * kk + lane / 32;
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const uint32_t r = wm * TM + i * 32 + lane % 32;
+            f.a[i] = *reinterpret_cast<const v4i*>(&As[r * P + (ch ^ swz(r)) * 16]);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const uint32_t r = wn * TN + j * 32 + lane % 32;
+            f.b[j] = *reinterpret_cast<const v4i*>(&Bs[r * P + (ch ^ swz(r)) * 16]);
+        }
+    };
+    auto mma = [&](const Frags<G>& f) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
     };
 
     const uint32_t nk = (K + BK - 1) / BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (uint32_t kt = 0; kt < nk; kt++) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * BK);
-#pragma unroll
-        for (int kk = 0; kk < BK / 64; kk++) {
-            v4i a[FM], b[FN];
-            const uint32_t kofs = kk * 64 + (lane / 16) * 16;
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-                a[i] = *reinterpret_cast<const v4i*>(&As[buf][(wm * TM + i * 16 + lane % 16) * kPitch + kofs]);
-#pragma unroll
-            for (int j = 0; j < FN; j++)
-                b[j] = *reinterpret_cast<const v4i*>(&Bs[buf][(wn * TN + j * 16 + lane % 16) * kPitch + kofs]);
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-                for (int j = 0; j < FN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+    auto mainloop = [&](auto fast_tag) {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        auto gload = [&](uint32_t k0, Ld& g) {
+            if constexpr (FAST) gload_fast(k0, g);
+            else gload_edge(k0, g);
+        };
+        // Prologue: tiles 0 and 1 into LDS stages 0 and 1, tiles 2 and 3
+        // in flight in the two load sets.
+        Ld g0, g1;
+        gload(0, g0);
+        sstore(0, g0);
+        if (nk > 1) {
+            gload(BK, g1);
+            sstore(1, g1);
         }
-        if (kt + 1 < nk) sstore(buf ^ 1);
+        if (nk > 2) gload(2 * BK, g0);
+        if (nk > 3) gload(3 * BK, g1);
         __syncthreads();
-    }
+        Frags<G> f0, f1;
+        fload(0, 0, f0);
+        // Iteration kt (f0 holds tile kt's first 32-k step on entry, the
+        // load set in use holds tile kt+2): store tile kt+2 to LDS, fetch
+        // tile kt+4, then alternate fragment reads and MFMAs one 32-k step
+        // ahead, ending with f0 holding tile kt+1's first step.  The barrier
+        // protects the stage that a later iteration overwrites.
+        //
+        // Steady state unrolled by the stage count, so every stage index is
+        // a compile-time constant (LDS addresses fold into immediates); the
+        // two load sets alternate at compile time.
+        uint32_t kt = 0;
+        for (; kt + S + 3 < nk; kt += S) {
+            static_for<S>([&](auto U) {
+                constexpr int u = decltype(U)::value;
+                Ld& g = (u & 1) ? g1 : g0;
+                sstore((u + 2) % S, g);
+                gload((kt + u + 4) * BK, g);
+                fload(u, 1, f1);
+                mma(f0);
+                fload((u + 1) % S, 0, f0);
+                mma(f1);
+                __syncthreads();
+            });
+        }
+        // Last iterations: identical code each time (the load sets rotate by
+        // value), so the accumulators' dataflow never forks -- a fork makes
+        // the register allocator give them a second home.  On entry g0
+        // holds tile kt+2 and g1 tile kt+3.
+        for (; kt < nk; kt++) {
+            if (kt + 2 < nk) sstore((kt + 2) % S, g0);
+            g0 = g1;
+            if (kt + 4 < nk) gload((kt + 4) * BK, g1);
+            fload(kt % S, 1, f1);
+            mma(f0);
+            if (kt + 1 < nk) fload((kt + 1) % S, 0, f0);
+            mma(f1);
+            __syncthreads();
+        }
+    };
+    if (ALIGNED && K % BK == 0 && (uint64_t)M * lda < (1ull << 31) && (uint64_t)N * ldb < (1ull << 31))
+        mainloop(std::true_type{});
+    else
+        mainloop(std::false_type{});
 
-    // D layout of a 16x16 MFMA block: lane holds column lane%16, rows
-    // 4*(lane/16) + r in element r.
-#pragma unroll
-    for (int i = 0; i < FM; i++)
+    // Epilogue through LDS: each wave stages one 32-row block-row of its
+    // tile, then reads it back row-major so every lane owns 4 consecutive
+    // columns and stores them with one 128-bit write.  The block-row index
+    // is a compile-time constant (static_for), so the accumulators are never
+    // indexed dynamically (which would force them out of registers).
+    int32_t* stage = reinterpret_cast<int32_t*>(smem) + wave * 32 * G::kEpiPitch;
+    static_for<FM>([&](auto I) {
+        constexpr int i = decltype(I)::value;
 #pragma unroll
         for (int j = 0; j < FN; j++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                uint32_t m = m0 + wm * TM + i * 16 + 4 * (lane / 16) + r;
-                uint32_t n = n0 + wn * TN + j * 16 + lane % 16;
-                if (m < M && n < N) epilogue_store<EPI>(p, m, n, acc[i][j][r]);
-            }
+            for (int r = 0; r < 16; r++)
+                stage[(8 * (r / 4) + 4 * (lane / 32) + r % 4) * G::kEpiPitch + j * 32 + lane % 32] = acc[i][j][r];
+        __syncthreads();
+        constexpr int kLanesPerRow = TN / 4;
+        constexpr int kRowsPerPass = 64 / kLanesPerRow;
+        for (int rr = 0; rr < 32; rr += kRowsPerPass) {
+            const uint32_t row = rr + lane / kLanesPerRow, col = (lane % kLanesPerRow) * 4;
+            const v4i v = *reinterpret_cast<const v4i*>(&stage[row * G::kEpiPitch + col]);
+            const uint32_t m = m0 + wm * TM + i * 32 + row, n = n0 + wn * TN + col;
+            if (m < M && n < N) epilogue_store4<EPI>(p, m, n, N, v);
+        }
+        __syncthreads();
+    });
 }
 
 // --------------------------------------------------- skinny (M <= 16) GEMM
 
-constexpr int kSkWaves = 8, kSkThreads = 64 * kSkWaves, kSkUnroll = 8;
+constexpr int kSkWaves = 16, kSkThreads = 64 * kSkWaves, kSkUnroll = 8, kSkPanels = 2;
 
 template <int EPI, bool ALIGNED>
 __global__ void __launch_bounds__(kSkThreads) k_gemv_i8_nt(const int8_t* __restrict__ A, uint32_t lda,
                                                            const int8_t* __restrict__ B, uint32_t ldb,
                                                            uint32_t M, uint32_t N, uint32_t K,
                                                            uint32_t k_per_wave, EpiParams p) {
-    __shared__ v4i red[kSkWaves][64];
+    __shared__ v4i red[kSkWaves][kSkPanels][64];
     const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-    const uint32_t n0 = blockIdx.x * 16;
-    const uint32_t ra = lane % 16, rb = n0 + lane % 16;
+    const uint32_t n0 = blockIdx.x * (16 * kSkPanels);
+    const uint32_t ra = lane % 16;
     const uint32_t kl = (lane / 16) * 16;
     const uint32_t kbeg = wave * k_per_wave;
     const uint32_t kend = kbeg + k_per_wave < K ? kbeg + k_per_wave : K;
 
-    v4i acc = {0, 0, 0, 0};
+    v4i acc[kSkPanels];
+#pragma unroll
+    for (int q = 0; q < kSkPanels; q++) acc[q] = (v4i){0, 0, 0, 0};
     for (uint32_t k = kbeg; k < kend; k += 64 * kSkUnroll) {
-        v4i a[kSkUnroll], b[kSkUnroll];
+        v4i a[kSkUnroll], b[kSkPanels][kSkUnroll];
 #pragma unroll
         for (int u = 0; u < kSkUnroll; u++) {
-            uint32_t kk = k + u * 64 + kl;
-            bool in = k + u * 64 < kend;
-            b[u] = in ? load_chunk<ALIGNED>(B, ldb, N, K, rb, kk) : (v4i){0, 0, 0, 0};
+            const uint32_t kk = k + u * 64 + kl;
+            const bool in = k + u * 64 < kend;
+#pragma unroll
+            for (int q = 0; q < kSkPanels; q++)
+                b[q][u] = in ? load_chunk<ALIGNED>(B, ldb, N, K, n0 + q * 16 + lane % 16, kk) : (v4i){0, 0, 0, 0};
             a[u] = in ? load_chunk<ALIGNED>(A, lda, M, K, ra, kk) : (v4i){0, 0, 0, 0};
         }
 #pragma unroll
-        for (int u = 0; u < kSkUnroll; u++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+        for (int u = 0; u < kSkUnroll; u++)
+#pragma unroll
+            for (int q = 0; q < kSkPanels; q++)
+                acc[q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[q][u], acc[q], 0, 0, 0);
     }
-    red[wave][lane] = acc;
+#pragma unroll
+    for (int q = 0; q < kSkPanels; q++) red[wave][q][lane] = acc[q];
     __syncthreads();
-    if (wave != 0) return;
+    if (wave >= kSkPanels) return;
+    const int q = wave;
+    v4i s = red[0][q][lane];
 #pragma unroll
     for (int w = 1; w < kSkWaves; w++) {
-        v4i t = red[w][lane];
-        acc[0] = wrap_add(acc[0], t[0]);
-        acc[1] = wrap_add(acc[1], t[1]);
-        acc[2] = wrap_add(acc[2], t[2]);
-        acc[3] = wrap_add(acc[3], t[3]);
+        v4i t = red[w][q][lane];
+        s[0] = wrap_add(s[0], t[0]);
+        s[1] = wrap_add(s[1], t[1]);
+        s[2] = wrap_add(s[2], t[2]);
+        s[3] = wrap_add(s[3], t[3]);
     }
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        uint32_t m = 4 * (lane / 16) + r, n = n0 + lane % 16;
-        if (m < M && n < N) epilogue_store<EPI>(p, m, n, acc[r]);
+        uint32_t m = 4 * (lane / 16) + r, n = n0 + q * 16 + lane % 16;
+        if (m < M && n < N) epilogue_store<EPI>(p, m, n, s[r]);
     }
 }
 
@@ -271,6 +512,31 @@ __global__ void __launch_bounds__(256) k_rowsum_i8(const int8_t* __restrict__ X,
 
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
+// Tile configuration: the 256 x 256 tile when it still gives every CU at
+// least two tiles, else 128 x 128.  RPLHIP_I8_TILE=small|big overrides (for
+// tuning sweeps only).
+bool use_big_tile(uint32_t M, uint32_t N) {
+    static const char* env = getenv("RPLHIP_I8_TILE");
+    if (env && env[0] == 's') return false;
+    if (env && env[0] == 'b') return true;
+    uint64_t tiles = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
+    return tiles >= 2ull * rplhip::cu_count();
+}
+
+template <class G, int EPI>
+int launch_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_t M, uint32_t N, uint32_t K,
+              const EpiParams& p, bool al, hipStream_t s) {
+    uint64_t tiles = (uint64_t)((M + G::BM - 1) / G::BM) * ((N + G::BN - 1) / G::BN);
+    if (tiles > 0x7fffffffull) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "int8 GEMM: %u x %u too large", M, N);
+    if (al)
+        hipLaunchKernelGGL((k_gemm_i8_nt<G, EPI, true>), dim3((uint32_t)tiles), dim3(G::kThreads), 0, s, A, lda, B,
+                           ldb, M, N, K, p);
+    else
+        hipLaunchKernelGGL((k_gemm_i8_nt<G, EPI, false>), dim3((uint32_t)tiles), dim3(G::kThreads), 0, s, A, lda, B,
+                           ldb, M, N, K, p);
+    return rplhip::check_launch("int8 GEMM");
+}
+
 template <int EPI>
 int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_t M, uint32_t N, uint32_t K,
            const EpiParams& p, hipStream_t s) {
@@ -279,7 +545,7 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
         // Split K over the block's waves in 64-byte steps.
         uint32_t kpw = (K + kSkWaves - 1) / kSkWaves;
         kpw = (kpw + 63) / 64 * 64;
-        dim3 grid((N + 15) / 16);
+        dim3 grid((N + 16 * kSkPanels - 1) / (16 * kSkPanels));
         if (al)
             hipLaunchKernelGGL((k_gemv_i8_nt<EPI, true>), grid, dim3(kSkThreads), 0, s, A, lda, B, ldb, M, N, K,
                                kpw, p);
@@ -288,13 +554,10 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
                                kpw, p);
         return rplhip::check_launch("skinny int8 GEMM");
     }
-    dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-    if (grid.y > 65535) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "int8 GEMM: M=%u too large", M);
-    if (al)
-        hipLaunchKernelGGL((k_gemm_i8_nt<EPI, true>), grid, dim3(kThreads), 0, s, A, lda, B, ldb, M, N, K, p);
-    else
-        hipLaunchKernelGGL((k_gemm_i8_nt<EPI, false>), grid, dim3(kThreads), 0, s, A, lda, B, ldb, M, N, K, p);
-    return rplhip::check_launch("int8 GEMM");
+    // Odd shapes (byte-wise loads) always take the small tile: the big one
+    // has no registers to spare for them.
+    if (al && use_big_tile(M, N)) return launch_nt<CfgBig, EPI>(A, lda, B, ldb, M, N, K, p, al, s);
+    return launch_nt<CfgSmall, EPI>(A, lda, B, ldb, M, N, K, p, al, s);
 }
 
 int transpose_b(const int8_t* B, uint32_t K, uint32_t N, int8_t* Bt, hipStream_t s) {
