@@ -475,23 +475,135 @@ __global__ void __launch_bounds__(kSkThreads) k_gemv_i8_nt(const int8_t* __restr
     }
 }
 
-// ----------------------------------------------------- helpers for gemm_int8
+// ------------------------------------------- decode-sized (M <= 4) GEMM
 
-// Bt[n][k] = B[k][n] through a 64x64 LDS tile.
-__global__ void __launch_bounds__(256) k_transpose_i8(const int8_t* __restrict__ B, uint32_t K, uint32_t N,
-                                                      int8_t* __restrict__ Bt) {
-    __shared__ int8_t t[64][65];
-    const uint32_t k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-    for (uint32_t i = threadIdx.x; i < 64 * 64; i += 256) {
-        uint32_t r = i / 64, c = i % 64;
-        uint32_t k = k0 + r, n = n0 + c;
-        t[r][c] = (k < K && n < N) ? B[(uint64_t)k * N + n] : (int8_t)0;
+// For M <= 4 an MFMA operand would be mostly padding and its lane layout
+// (16 rows per load) scatters each HBM load over 16 rows; instead each wave
+// streams whole rows of B with v_dot4_i32_i8: one load instruction moves
+// 1 KB contiguous (64 lanes x 16 bytes) of one row, and a wave issues all
+// the loads of an 8 KB k-slice of its rows before consuming any, so HBM
+// latency is paid once per slice.  A (M x K, at most 64 KiB) is staged once
+// per block in LDS.  Block: 8 waves x ROWS rows of B.
+constexpr int kDvWaves = 8, kDvThreads = 64 * kDvWaves, kDvSlice = 8;  // 8 x 1 KB per row per slice
+constexpr uint32_t kDvMaxA = 64 * 1024;
+
+template <int EPI, int MM, int ROWS, bool ALIGNED>
+__global__ void __launch_bounds__(kDvThreads) k_gemv_i8_dot4(const int8_t* __restrict__ A, uint32_t lda,
+                                                             const int8_t* __restrict__ B, uint32_t ldb,
+                                                             uint32_t M, uint32_t N, uint32_t K, EpiParams p) {
+    extern __shared__ __attribute__((aligned(16))) int8_t xs[];  // [MM][Kp], Kp = K rounded up to 1024
+    const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const uint32_t Kp = (K + 1023) / 1024 * 1024;
+    const uint32_t n0 = (blockIdx.x * kDvWaves + wave) * ROWS;
+    // Issue the first slice of B before staging A, so both are in flight.
+    v4i w[ROWS][kDvSlice];
+    auto wload = [&](uint32_t k) {
+#pragma unroll
+        for (int u = 0; u < kDvSlice; u++)
+#pragma unroll
+            for (int r = 0; r < ROWS; r++) {
+                const uint32_t kk = k + u * 1024 + lane * 16;
+                w[r][u] = kk < Kp ? load_chunk<ALIGNED>(B, ldb, N, K, n0 + r, kk) : (v4i){0, 0, 0, 0};
+            }
+    };
+    wload(0);
+    for (uint32_t c = threadIdx.x; c < MM * Kp / 16; c += kDvThreads) {
+        const uint32_t m = c / (Kp / 16), k = (c % (Kp / 16)) * 16;
+        const v4i v = m < M ? load_chunk<ALIGNED>(A, lda, M, K, m, k) : (v4i){0, 0, 0, 0};
+        *reinterpret_cast<v4i*>(&xs[m * Kp + k]) = v;
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < 64 * 64; i += 256) {
-        uint32_t r = i / 64, c = i % 64;  // r: n offset, c: k offset
-        uint32_t n = n0 + r, k = k0 + c;
-        if (n < N && k < K) Bt[(uint64_t)n * K + k] = t[c][r];
+    int32_t acc[MM][ROWS];
+#pragma unroll
+    for (int m = 0; m < MM; m++)
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) acc[m][r] = 0;
+    for (uint32_t k = 0; k < Kp; k += 1024 * kDvSlice) {
+        if (k > 0) wload(k);
+#pragma unroll
+        for (int u = 0; u < kDvSlice; u++) {
+            const uint32_t kk = k + u * 1024 + lane * 16;
+            if (kk >= Kp) break;
+#pragma unroll
+            for (int m = 0; m < MM; m++) {
+                const v4i x = *reinterpret_cast<const v4i*>(&xs[m * Kp + kk]);
+#pragma unroll
+                for (int r = 0; r < ROWS; r++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[m][r] = __builtin_amdgcn_sdot4(x[e], w[r][u][e], acc[m][r], false);
+            }
+        }
+    }
+    // Wave-wide int32 sums (wrapping, so any order is exact).
+#pragma unroll
+    for (int m = 0; m < MM; m++)
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) {
+            int32_t v = acc[m][r];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v = wrap_add(v, __shfl_xor(v, off));
+            acc[m][r] = v;
+        }
+    if (lane < (uint32_t)(MM * ROWS)) {
+        const uint32_t m = lane / ROWS, r = lane % ROWS;
+        int32_t v = 0;
+#pragma unroll
+        for (int mm = 0; mm < MM; mm++)
+#pragma unroll
+            for (int rr = 0; rr < ROWS; rr++)
+                if (mm == (int)m && rr == (int)r) v = acc[mm][rr];
+        if (m < M && n0 + r < N) epilogue_store<EPI>(p, m, n0 + r, v);
+    }
+}
+
+// ----------------------------------------------------- helpers for gemm_int8
+
+// Bt[n][k] = B[k][n], one 64 x 64-byte tile per block.  Thread (kq, n4)
+// loads the 4 dwords B[4kq..4kq+3][4n4..4n4+3] (each load instruction of a
+// wave covers 4 rows x 64 contiguous bytes), transposes the 4 x 4 bytes in
+// registers, and parks the 4 resulting dwords in an LDS tile laid out
+// [n][k-dword] with a 17-dword pitch (conflict-free for this write pattern);
+// the tile is then written out row by row, 64 contiguous bytes per 16 lanes.
+__global__ void __launch_bounds__(256) k_transpose_i8(const int8_t* __restrict__ B, uint32_t K, uint32_t N,
+                                                      int8_t* __restrict__ Bt) {
+    __shared__ uint32_t t[64][17];
+    const uint32_t k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const uint32_t n4 = threadIdx.x % 16, kq = threadIdx.x / 16;
+    const bool full = k0 + 64 <= K && n0 + 64 <= N && N % 4 == 0 && K % 4 == 0 && (((uintptr_t)B) & 3) == 0 &&
+                      (((uintptr_t)Bt) & 3) == 0;
+    uint32_t d[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t k = k0 + 4 * kq + i, n = n0 + 4 * n4;
+        if (full) {
+            d[i] = *reinterpret_cast<const uint32_t*>(B + (uint64_t)k * N + n);
+        } else {
+            uint32_t v = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+                if (k < K && n + b < N) v |= (uint32_t)(uint8_t)B[(uint64_t)k * N + n + b] << (8 * b);
+            d[i] = v;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t e = ((d[0] >> (8 * j)) & 0xff) | (((d[1] >> (8 * j)) & 0xff) << 8) |
+                           (((d[2] >> (8 * j)) & 0xff) << 16) | (((d[3] >> (8 * j)) & 0xff) << 24);
+        t[4 * n4 + j][kq] = e;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t r = threadIdx.x / 16 + 16 * i, c = threadIdx.x % 16;
+        const uint32_t n = n0 + r, k = k0 + 4 * c;
+        const uint32_t v = t[r][c];
+        if (full) {
+            *reinterpret_cast<uint32_t*>(Bt + (uint64_t)n * K + k) = v;
+        } else if (n < N) {
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+                if (k + b < K) Bt[(uint64_t)n * K + k + b] = (int8_t)(v >> (8 * b));
+        }
     }
 }
 
@@ -541,6 +653,28 @@ template <int EPI>
 int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_t M, uint32_t N, uint32_t K,
            const EpiParams& p, hipStream_t s) {
     bool al = K % 16 == 0 && lda % 16 == 0 && ldb % 16 == 0 && aligned16(A) && aligned16(B);
+    const uint32_t Kp = (K + 1023) / 1024 * 1024;
+    if (M <= 4 && (uint64_t)4 * Kp <= kDvMaxA) {
+        size_t lds = (size_t)(M <= 1 ? 1 : M <= 2 ? 2 : 4) * Kp;
+#define RPL_DV(MM, ROWS)                                                                                           \
+    do {                                                                                                           \
+        dim3 grid((N + kDvWaves * ROWS - 1) / (kDvWaves * ROWS));                                                  \
+        if (al)                                                                                                    \
+            hipLaunchKernelGGL((k_gemv_i8_dot4<EPI, MM, ROWS, true>), grid, dim3(kDvThreads), lds, s, A, lda, B,  \
+                               ldb, M, N, K, p);                                                                   \
+        else                                                                                                       \
+            hipLaunchKernelGGL((k_gemv_i8_dot4<EPI, MM, ROWS, false>), grid, dim3(kDvThreads), lds, s, A, lda, B, \
+                               ldb, M, N, K, p);                                                                   \
+    } while (0)
+        if (M <= 1)
+            RPL_DV(1, 1);
+        else if (M <= 2)
+            RPL_DV(2, 1);
+        else
+            RPL_DV(4, 2);
+#undef RPL_DV
+        return rplhip::check_launch("decode int8 GEMM");
+    }
     if (M <= 16) {
         // Split K over the block's waves in 64-byte steps.
         uint32_t kpw = (K + kSkWaves - 1) / kSkWaves;
