@@ -1,33 +1,41 @@
-// INT8 GEMMs on gfx950 i8 MFMA (v_mfma_i32_16x16x64_i8), int32 accumulation.
+// INT8 GEMMs on gfx950, int32 accumulation.
 //
 // Core kernel: NT layout (A [M,K] and B [N,K], both k-contiguous), which is
 // what the MFMA operands want: every lane feeds 16 consecutive k bytes of one
-// row.  Block tile BM x BN x BK staged through LDS (double-buffered, rows
-// padded by 16 bytes so the lanes of a ds_read_b128 phase hit distinct
-// banks); 4 waves (2 x 2), each owning a (BM/2) x (BN/2) sub-tile of 16x16
-// MFMA blocks.  The large configuration (256 x 256, 128 x 128 per wave, the
-// 256 int32 accumulators living in AGPRs) halves the LDS bytes read per MFMA
-// op compared with 64 x 64 wave tiles, which is what bounds this kernel.
-// Global loads are 128-bit and coalesced along k.  Tiles are visited in an
-// XCD-aware grouped order: workgroups are dispatched round-robin over the 8
-// XCDs, so consecutive tile indices are remapped onto one XCD and grouped
-// 8 tile-rows at a time, which keeps the A and B panels the XCD's 32 CUs
-// share resident in that XCD's L2.
+// row.  v_mfma_i32_32x32x32_i8 (65536 ops per 32-cycle issue; it sustains
+// close to peak from one wave per SIMD, where 16x16x64 with the same
+// accumulator count does not).  Block tile BM x BN x 64 staged through LDS in
+// 4 stages of 64-byte rows whose four 16-byte chunks are XOR-swizzled, so both
+// the 128-bit fragment reads and the 128-bit tile writes are conflict-free;
+// 4 waves (2 x 2), each owning a (BM/2) x (BN/2) sub-tile of 32x32 MFMA
+// blocks.  The large configuration (256 x 256, 128 x 128 per wave, the 256
+// int32 accumulators living in AGPRs) halves the LDS bytes read per MFMA op
+// compared with 64 x 64 wave tiles.  Pipeline: HBM loads two tiles ahead (two
+// register sets), LDS one tile ahead, fragments double-buffered per 32-k step,
+// one barrier per tile.  Global loads are 128-bit raw buffer loads whose
+// resource ends at the last existing row, so M and N edges zero-fill in
+// hardware.  Tiles are visited in an XCD-aware grouped order: workgroups are
+// dispatched round-robin over the 8 XCDs, so consecutive tile indices are
+// remapped onto one XCD and grouped 8 tile-rows at a time, which keeps the A
+// and B panels the XCD's 32 CUs share resident in that XCD's L2.
 //
 // The epilogue is fused and selected at compile time:
 //   kRaw     : out = acc + bias[n]                      (linear_int8)
 //   kRequant : out = x86((int32)roundf(((float)acc*sa)*sb/sc)), optional
 //              zero-point correction                     (gemm_int8)
 //   kDequant : y = ((float)acc * sx[m|0]) * sw[n|0]      (fused fp32 output)
+// It is staged through LDS so every lane writes four consecutive outputs.
 //
 // gemm_int8's B is [K,N] (n-contiguous); it is first transposed into a
 // stream-ordered workspace so the NT core serves both layouts.
 //
-// M <= 16 (decode-style skinny GEMMs) runs a separate bandwidth kernel: 16
-// waves per block split K, each lane streams 16-byte chunks of B straight
-// from HBM into MFMA operands (A, padded to 16 rows, is the other operand and
-// is reused across the block's two 16-row B panels), and the 16 partial
-// tiles are reduced through LDS before the epilogue.
+// Decode shapes: M <= 4 runs a VALU kernel (v_dot4_i32_i8) in which each wave
+// streams whole rows of B, 1 KB per load instruction, with A staged once per
+// block in LDS.  4 < M <= 16 runs an MFMA bandwidth kernel: 16 waves per block
+// split K, each lane streams 16-byte chunks of B straight from HBM into MFMA
+// operands (A, padded to 16 rows, is the other operand and is reused across
+// the block's two 16-row B panels), and the 16 partial tiles are reduced
+// through LDS before the epilogue.
 #include <math.h>
 #include <stdlib.h>
 
