@@ -54,7 +54,7 @@ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
-enum Epi { kRaw = 0, kRequant = 1, kDequant = 2 };
+enum Epi { kRaw = 0, kRequant = 1, kDequant = 2, kRequantPow2 = 3 };
 
 struct EpiParams {
     // kRaw
@@ -66,6 +66,9 @@ struct EpiParams {
     const int32_t* rowsum_a;  // [M], NULL when zb == 0
     const int32_t* rowsum_b;  // [N], NULL when za == 0
     int32_t kzz;              // K*za*zb (wrapping)
+    // kRequantPow2 (no zero points, sc = +-2^k with 1/sc exact): x / sc is
+    // computed as x * inv_sc, which rounds the same real number once.
+    float inv_sc;
     // kDequant
     const float* sx;
     const float* sw;
@@ -87,6 +90,9 @@ __device__ __forceinline__ void epilogue_store(const EpiParams& p, uint32_t m, u
         if (p.rowsum_b) v = wrap_add(v, -wrap_mul(p.za, p.rowsum_b[n]));
         v = wrap_add(v, p.kzz);
         float result = (float)v * p.sa * p.sb / p.sc;  // ops_extended.c:119
+        p.out_i32[o] = x86_cvt_i32(roundf(result));
+    } else if (EPI == kRequantPow2) {
+        float result = (float)acc * p.sa * p.sb * p.inv_sc;
         p.out_i32[o] = x86_cvt_i32(roundf(result));
     } else {
         float v = (float)acc * p.sx[p.sx_per_row ? m : 0];
@@ -165,6 +171,19 @@ __device__ __forceinline__ uint32_t swz(uint32_t r) { return ((r >> 1) ^ (r >> 3
 // swizzle, range-checked against num_records).
 constexpr int kBufferFlags = 0x00020000;
 
+// Raw buffer resource for `bytes` bytes at `base`.  The fields go through
+// readfirstlane so the resource is provably wave-uniform and lives in SGPRs:
+// a resource the compiler cannot prove uniform makes it wrap every buffer
+// load in a readfirstlane/compare/exec loop.  Callers pass values that are
+// uniform already (derived from blockIdx and kernel arguments).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t p = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+    const uint32_t n = __builtin_amdgcn_readfirstlane(bytes);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, (int)n, kBufferFlags);
+}
+
 template <int BM_, int BN_>
 struct Cfg {
     static constexpr int BM = BM_, BN = BN_, BK = 64;
@@ -219,6 +238,8 @@ __device__ __forceinline__ void epilogue_store4(const EpiParams& p, uint32_t m, 
             int32_t x = v[e];
             if (EPI == kRaw) {
                 if (p.bias) x = wrap_add(x, (int32_t)p.bias[n + e]);
+            } else if (EPI == kRequantPow2) {
+                x = x86_cvt_i32(roundf((float)x * p.sa * p.sb * p.inv_sc));
             } else {
                 if (p.rowsum_a) x = wrap_add(x, -wrap_mul(p.zb, p.rowsum_a[m]));
                 if (p.rowsum_b) x = wrap_add(x, -wrap_mul(p.za, p.rowsum_b[n + e]));
@@ -269,12 +290,8 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt(const int8_t* __restrict_
     const uint32_t voff_a = (tid / CPR) * lda + (tid % CPR) * 16;
     const uint32_t voff_b = (tid / CPR) * ldb + (tid % CPR) * 16;
     constexpr uint32_t kRowsPerLoad = G::kThreads / CPR;
-    const __amdgpu_buffer_rsrc_t rsrc_a =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(A + (uint64_t)m0 * lda), (short)0,
-                                          (int)((M > m0 ? M - m0 : 0) * lda), kBufferFlags);
-    const __amdgpu_buffer_rsrc_t rsrc_b =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(B + (uint64_t)n0 * ldb), (short)0,
-                                          (int)((N > n0 ? N - n0 : 0) * ldb), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rsrc_a = uniform_rsrc(A + (uint64_t)m0 * lda, (M > m0 ? M - m0 : 0) * lda);
+    const __amdgpu_buffer_rsrc_t rsrc_b = uniform_rsrc(B + (uint64_t)n0 * ldb, (N > n0 ? N - n0 : 0) * ldb);
     auto gload_fast = [&](uint32_t k0, Ld& g) {
 #pragma unroll
         for (int i = 0; i < G::kChunksA; i++)
@@ -422,6 +439,221 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt(const int8_t* __restrict_
             if (m < M && n < N) epilogue_store4<EPI>(p, m, n, N, v);
         }
         __syncthreads();
+    });
+}
+
+// ------------------------------------ NT core GEMM, direct-to-LDS pipeline
+
+// gfx9 s_waitcnt immediate: vmcnt in bits [3:0] and [15:14], expcnt [6:4],
+// lgkmcnt [11:8]; a field at its maximum does not wait.
+constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8); }
+
+namespace dma {
+constexpr int BM = 256, BN = 256, BK = 64, S = 4, kThreads = 256;
+constexpr int kTileBytes = BM * BK;          // one operand of one stage: 16 KB
+constexpr int kStageBytes = (BM + BN) * BK;  // 32 KB
+constexpr int kLoads = 4;                    // 1 KB loads per wave per operand per tile
+constexpr int kVmPerTile = 2 * kLoads;       // load instructions per wave per tile
+}  // namespace dma
+
+// Same tiles, MFMA and fused epilogues as k_gemm_i8_nt<CfgBig>, with the
+// HBM -> LDS copies done by the load unit itself (buffer_load_dwordx4 ...
+// lds): each instruction moves 16 rows x 64 bytes of a tile into 1 KB of
+// LDS, lane l writing bytes 16l..16l+15.  The XOR swizzle of the LDS rows is
+// produced by choosing which 16-byte chunk each lane fetches (lane l of a
+// load fetches chunk (l%4) ^ swz(row) of row l/4), so the fragment reads
+// stay conflict-free and no VGPRs or ds_write instructions stage the tiles.
+//
+// Pipeline over a ring of 4 LDS stages: tile kt+3 is requested while tile kt
+// is multiplied; one barrier per tile, placed between the two 32-k halves,
+// after which the wave's own copies of tile kt+1 have landed (explicit
+// vmcnt) and every wave has finished reading the stage that the next
+// iteration refills.  Rows past M / N are clamped to the last row (their
+// products are never stored), so no load leaves the operand.
+//
+// The epilogue stores straight from the accumulators: for each of the 16
+// result registers a wave writes two 128-byte row segments (32 lanes x 4
+// bytes each), so every store fills whole cache lines.
+//
+// Requires K % 64 == 0, 16-byte aligned operands and leading dimensions,
+// and operands below 2 GiB (32-bit buffer offsets).
+template <int EPI>
+__global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restrict__ A, uint32_t lda,
+                                                           const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
+                                                           uint32_t N, uint32_t K, EpiParams p) {
+    using namespace dma;
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[S * kStageBytes];
+
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t wm = wave / 2, wn = wave % 2;
+    uint32_t im, in;
+    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, im, in);
+    const uint32_t m0 = im * BM, n0 = in * BN;
+    const uint32_t rows_a = M - m0 < (uint32_t)BM ? M - m0 : BM;
+    const uint32_t rows_b = N - n0 < (uint32_t)BN ? N - n0 : BN;
+    const __amdgpu_buffer_rsrc_t rsrc_a = uniform_rsrc(A + (uint64_t)m0 * lda, rows_a * lda);
+    const __amdgpu_buffer_rsrc_t rsrc_b = uniform_rsrc(B + (uint64_t)n0 * ldb, rows_b * ldb);
+
+    // Source offsets of this lane's four A and four B copies (k added as the
+    // scalar offset).
+    uint32_t voff_a[kLoads], voff_b[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; i++) {
+        const uint32_t r = wave * 64 + i * 16 + lane / 4;
+        const uint32_t c = ((lane % 4) ^ swz(r)) * 16;
+        voff_a[i] = (r < rows_a ? r : rows_a - 1) * lda + c;
+        voff_b[i] = (r < rows_b ? r : rows_b - 1) * ldb + c;
+    }
+    auto issue = [&](uint32_t kt, uint32_t stage) {
+        int8_t* st = smem + stage * kStageBytes;
+#pragma unroll
+        for (int i = 0; i < kLoads; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr)(st + (wave * 64 + i * 16) * BK), 16,
+                                                     voff_a[i], kt * BK, 0, 0);
+#pragma unroll
+        for (int i = 0; i < kLoads; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr)(st + kTileBytes + (wave * 64 + i * 16) * BK),
+                                                     16, voff_b[i], kt * BK, 0, 0);
+    };
+
+    // Fragment reads: lane feeds row lane%32 of each 32-row block with chunk
+    // 2*kk + lane/32; the rows of a block differ from lane%32 by a multiple
+    // of 32, so the swizzle slot depends on the lane alone.
+    const uint32_t fr = lane % 32;
+    uint32_t foff[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) foff[kk] = fr * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
+    const uint32_t a_base = wm * 128 * BK, b_base = kTileBytes + wn * 128 * BK;
+    typedef Frags<CfgBig> F;
+    auto fload = [&](uint32_t stage, int kk, F& f) {
+        const int8_t* st = smem + stage * kStageBytes + foff[kk];
+#pragma unroll
+        for (int i = 0; i < 4; i++) f.a[i] = *reinterpret_cast<const v4i*>(st + a_base + i * 32 * BK);
+#pragma unroll
+        for (int j = 0; j < 4; j++) f.b[j] = *reinterpret_cast<const v4i*>(st + b_base + j * 32 * BK);
+    };
+    v16i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = (v16i){};
+    auto mma = [&](const F& f) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+    };
+
+    const uint32_t nk = K / BK;
+    // Prologue: tiles 0..2 requested, tile 0 landed and visible.
+    issue(0, 0);
+    if (nk > 1) issue(1, 1);
+    if (nk > 2) issue(2, 2);
+    if (nk > 2)
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kVmPerTile, 0));
+    else
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+    __builtin_amdgcn_s_barrier();
+    F f0, f1;
+    fload(0, 0, f0);
+
+    // Iteration kt: request tile kt+3 (into the stage tile kt-1 left), read
+    // tile kt's second half while multiplying its first, wait for tile kt+1
+    // and barrier, read tile kt+1's first half while multiplying kt's second.
+    //
+    // The steady state pins the instruction order (sched_group_barrier):
+    // each fragment read is issued between two MFMAs early in the half, the
+    // tile copies between the later MFMAs, so the MFMA pipe never waits on
+    // an LDS read issued just before it (left alone, the scheduler sinks
+    // every read to just before its first use and reuses its registers).
+    uint32_t kt = 0;
+    for (; kt + S + 3 <= nk; kt += S) {
+        static_for<S>([&](auto U) {
+            constexpr int u = decltype(U)::value;
+            __builtin_amdgcn_sched_barrier(0);
+            issue(kt + u + 3, (u + 3) % S);
+            fload(u, 1, f1);
+            mma(f0);
+            static_for<8>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            });
+            static_for<8>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // HBM -> LDS copy
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kVmPerTile, 0));
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            fload((u + 1) % S, 0, f0);
+            mma(f1);
+            static_for<8>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            });
+            static_for<8>([&](auto) { __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+    for (; kt < nk; kt++) {
+        if (kt + 3 < nk) issue(kt + 3, (kt + 3) % S);
+        fload(kt % S, 1, f1);
+        mma(f0);
+        if (kt + 3 < nk)
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kVmPerTile, 0));
+        else if (kt + 3 == nk)
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(kVmPerTile, 0));
+        else
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+        __builtin_amdgcn_s_barrier();
+        if (kt + 1 < nk) fload((kt + 1) % S, 0, f0);
+        mma(f1);
+    }
+
+    // Epilogue: result register r of lane l in block (i, j) is row
+    // 8*(r/4) + 4*(l/32) + r%4, column l%32.  Fully unrolled (the
+    // accumulators are only ever indexed by constants); values that depend
+    // on the column are loaded once per block column, those that depend on
+    // the row once per row; interior tiles skip the bounds checks.
+    const uint32_t mb = m0 + wm * 128 + 4 * (lane / 32), nb = n0 + wn * 128 + lane % 32;
+    const bool full = m0 + BM <= M && n0 + BN <= N;
+    int32_t cadd[4];  // kRaw: bias[n]
+    float cmul[4];    // kDequant: sw[n]
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t n = nb + j * 32;
+        cadd[j] = (EPI == kRaw && p.bias && n < N) ? (int32_t)p.bias[n] : 0;
+        cmul[j] = (EPI == kDequant && n < N) ? p.sw[p.sw_per_col ? n : 0] : 0.0f;
+    }
+    static_for<4>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        static_for<16>([&](auto R) {
+            constexpr int r = decltype(R)::value;
+            const uint32_t m = mb + i * 32 + 8 * (r / 4) + r % 4;
+            const bool row_ok = full || m < M;
+            const float rmul = (EPI == kDequant && row_ok) ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
+            static_for<4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                const uint32_t n = nb + j * 32;
+                if (full || (row_ok && n < N)) {
+                    const uint64_t o = (uint64_t)m * p.ldc + n;
+                    const int32_t a = acc[i][j][r];
+                    if constexpr (EPI == kRaw) {
+                        p.out_i32[o] = wrap_add(a, cadd[j]);
+                    } else if constexpr (EPI == kRequantPow2) {
+                        p.out_i32[o] = x86_cvt_i32(roundf((float)a * p.sa * p.sb * p.inv_sc));
+                    } else if constexpr (EPI == kDequant) {
+                        p.out_f32[o] = (float)a * rmul * cmul[j];
+                    } else {
+                        epilogue_store<EPI>(p, m, n, a);
+                    }
+                }
+            });
+        });
     });
 }
 
@@ -643,6 +875,13 @@ bool use_big_tile(uint32_t M, uint32_t N) {
     return tiles >= 2ull * rplhip::cu_count();
 }
 
+// The direct-to-LDS kernel serves the big tile unless RPLHIP_I8_DMA=0 (for
+// A/B timing only).
+bool use_dma() {
+    static const char* env = getenv("RPLHIP_I8_DMA");
+    return !(env && env[0] == '0');
+}
+
 template <class G, int EPI>
 int launch_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_t M, uint32_t N, uint32_t K,
               const EpiParams& p, bool al, hipStream_t s) {
@@ -698,8 +937,29 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
     }
     // Odd shapes (byte-wise loads) always take the small tile: the big one
     // has no registers to spare for them.
-    if (al && use_big_tile(M, N)) return launch_nt<CfgBig, EPI>(A, lda, B, ldb, M, N, K, p, al, s);
+    if (al && use_big_tile(M, N)) {
+        if (K % dma::BK == 0 && (uint64_t)M * lda < (1ull << 31) && (uint64_t)N * ldb < (1ull << 31) && use_dma()) {
+            const uint64_t tiles = (uint64_t)((M + dma::BM - 1) / dma::BM) * ((N + dma::BN - 1) / dma::BN);
+            hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI>), dim3((uint32_t)tiles), dim3(dma::kThreads), 0, s, A, lda, B,
+                               ldb, M, N, K, p);
+            return rplhip::check_launch("int8 GEMM");
+        }
+        return launch_nt<CfgBig, EPI>(A, lda, B, ldb, M, N, K, p, al, s);
+    }
     return launch_nt<CfgSmall, EPI>(A, lda, B, ldb, M, N, K, p, al, s);
+}
+
+// True (and *inv = 1/sc) when sc = +-2^k is a normal float whose reciprocal
+// is exactly representable: then x / sc and x * (1/sc) are both the
+// correctly rounded value of the same real number, for every x (overflow,
+// subnormal results, infinities and NaN included).
+bool exact_reciprocal(float sc, float* inv) {
+    if (!isfinite(sc) || sc == 0.0f) return false;
+    int e;
+    const float m = frexpf(fabsf(sc), &e);  // |sc| = m * 2^e, m in [0.5, 1)
+    if (m != 0.5f || e - 1 < -126) return false;
+    *inv = ldexpf(sc > 0 ? 1.0f : -1.0f, 1 - e);
+    return true;
 }
 
 int transpose_b(const int8_t* B, uint32_t K, uint32_t N, int8_t* Bt, hipStream_t s) {
@@ -778,7 +1038,12 @@ int rplhip_gemm_int8(const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, u
         hipLaunchKernelGGL(k_rowsum_i8, dim3(N), dim3(256), 0, s, Bt, N, K, (int32_t*)p.rowsum_b);
         st = check_launch("int8 column sums");
     }
-    if (!st) st = run_nt<kRequant>(A, K, Bt, K, M, N, K, p, s);
+    if (!st) {
+        if (za == 0 && zb == 0 && exact_reciprocal(sc, &p.inv_sc))
+            st = run_nt<kRequantPow2>(A, K, Bt, K, M, N, K, p, s);
+        else
+            st = run_nt<kRequant>(A, K, Bt, K, M, N, K, p, s);
+    }
     ws_free(ws, s);
     return st;
 }

@@ -203,3 +203,60 @@ def test_config4_int8_8192(gpu, orc):
     assert np.abs(a64).max() < 2 ** 24  # exact through the float requant with unit scales
     assert np.array_equal(a64.sum(1), qa.astype(np.int64) @ qb.astype(np.int64).sum(1))
     assert np.array_equal(a64.sum(0), qb.astype(np.int64).T @ qa.astype(np.int64).sum(0))
+
+
+def _requant_f32(acc, sa, sb, sc):
+    """x86((int32)roundf(((float)acc * sa) * sb / sc)) in numpy float32 (IEEE,
+    one rounding per operation, as the reference at ops_extended.c:119)."""
+    with np.errstate(all="ignore"):
+        x = ((acc.astype(np.float32) * np.float32(sa)) * np.float32(sb)) / np.float32(sc)
+        t = np.trunc(x)
+        r = np.where(np.abs(x - t) >= np.float32(0.5), t + np.sign(x), t)  # roundf: ties away from zero
+        ok = (r >= -2.0 ** 31) & (r < 2.0 ** 31)
+    out = np.full(acc.shape, np.iinfo(np.int32).min, np.int32)
+    out[ok] = r[ok].astype(np.int64).astype(np.int32)
+    return out
+
+
+# Shapes with >= 2 tiles of 256 x 256 per CU take the direct-to-LDS kernel
+# (k_gemm_i8_nt_dma); K = 448 and 832 run its steady-state loop and tails of
+# 3 and 5 tiles; the first shape has ragged edges in M and N.
+BIG = [(5890, 5900, 832), (6144, 6144, 448)]
+
+
+@pytest.mark.parametrize("M,N,K", BIG)
+def test_big_tile_int8_paths(gpu, orc, M, N, K):
+    lib = gpu
+    rng = np.random.default_rng(M + K)
+    A = np.clip(np.rint(rng.normal(0, 24, (M, K))), -127, 127).astype(np.int8)
+    Bt = np.clip(np.rint(rng.normal(0, 24, (N, K))), -127, 127).astype(np.int8)
+    B = np.ascontiguousarray(Bt.T)
+    dA, dB, dBt = up(A), up(B), up(Bt)
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(N).choice(M, 6, replace=False)]))
+    # linear_int8 (raw int32): sampled rows vs the oracle, every row and column by exact sums.
+    acc_d = empty((M, N), np.int32)
+    say("big-tile linear_int8", M, N, K)
+    rpl_amd.check(lib.rplhip_linear_int8(dA.ptr, dBt.ptr, None, acc_d.ptr, M, K, N, None))
+    acc = down(acc_d, np.int32, (M, N))
+    assert bits_equal(acc[rows], orc.linear_int8(np.ascontiguousarray(A[rows]), Bt, None, len(rows), K, N))
+    a64 = acc.astype(np.int64)
+    assert np.array_equal(a64.sum(1), A.astype(np.int64) @ Bt.astype(np.int64).sum(0))
+    assert np.array_equal(a64.sum(0), Bt.astype(np.int64) @ A.astype(np.int64).sum(0))
+    # gemm_int8 requant: power-of-two sc (exact-reciprocal epilogue) and a generic sc.
+    for sa, sb, sc in ((0.013, 0.7, 0.25), (1.5, -3.0, -4.0), (2.0 ** 20, 2.0 ** 20, 2.0 ** -100), (0.013, 0.7, 0.3)):
+        out = empty((M, N), np.int32)
+        say("big-tile gemm_int8", M, N, K, sa, sb, sc)
+        rpl_amd.check(lib.rplhip_gemm_int8(dA.ptr, dB.ptr, out.ptr, M, N, K, sa, sb, sc, 0, 0, None))
+        got = down(out, np.int32, (M, N))
+        assert bits_equal(got, _requant_f32(acc, sa, sb, sc))
+        ref = orc.gemm_int8(np.ascontiguousarray(A[rows]), B, len(rows), N, K, sa, sb, sc)
+        assert bits_equal(got[rows], ref)
+    # linear_int8_dequant: per-row x scales, per-column w scales, fp32 out.
+    sx = (rng.random(M).astype(np.float32) + 0.5) * np.float32(0.01)
+    sw = (rng.random(N).astype(np.float32) + 0.5) * np.float32(0.02)
+    dsx, dsw, Y = up(sx), up(sw), empty((M, N), np.float32)
+    say("big-tile linear_int8_dequant", M, N, K)
+    rpl_amd.check(lib.rplhip_linear_int8_dequant(dA.ptr, dsx.ptr, 1, dBt.ptr, dsw.ptr, 1, Y.ptr, M, K, N, None))
+    y = down(Y, np.float32, (M, N))
+    assert bits_equal(y, (acc.astype(np.float32) * sx[:, None]) * sw[None, :])
+    assert bits_equal(y[rows], orc.dequant_acc(acc[rows], sx[rows], True, sw, True))
