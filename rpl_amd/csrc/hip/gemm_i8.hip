@@ -442,14 +442,82 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt(const int8_t* __restrict_
     });
 }
 
+// Fused epilogue straight from MFMA accumulators: FM x FN blocks of 32x32;
+// result register r of lane l in block (i, j) is row mb + i*32 + 8*(r/4) +
+// r%4 and column nb + j*32, where mb = tile row + 4*(l/32) and nb = tile
+// column + l%32.  Fully unrolled (the accumulators are only ever indexed by
+// constants); values that depend on the column are loaded once per block
+// column, those that depend on the row once per row; interior tiles (`full`)
+// skip the bounds checks.  Each store instruction writes two 128-byte row
+// segments.
+template <int EPI, int FM, int FN>
+__device__ __forceinline__ void epilogue_tile(const EpiParams& p, const v16i (&acc)[FM][FN], uint32_t mb,
+                                              uint32_t nb, uint32_t M, uint32_t N, bool full) {
+    int32_t cadd[FN];  // kRaw: bias[n]
+    float cmul[FN];    // kDequant: sw[n]
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const uint32_t n = nb + j * 32;
+        cadd[j] = (EPI == kRaw && p.bias && n < N) ? (int32_t)p.bias[n] : 0;
+        cmul[j] = (EPI == kDequant && n < N) ? p.sw[p.sw_per_col ? n : 0] : 0.0f;
+    }
+    static_for<FM>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        static_for<16>([&](auto R) {
+            constexpr int r = decltype(R)::value;
+            const uint32_t m = mb + i * 32 + 8 * (r / 4) + r % 4;
+            const bool row_ok = full || m < M;
+            const float rmul = (EPI == kDequant && row_ok) ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
+            static_for<FN>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                const uint32_t n = nb + j * 32;
+                if (full || (row_ok && n < N)) {
+                    const uint64_t o = (uint64_t)m * p.ldc + n;
+                    const int32_t a = acc[i][j][r];
+                    if constexpr (EPI == kRaw) {
+                        p.out_i32[o] = wrap_add(a, cadd[j]);
+                    } else if constexpr (EPI == kRequantPow2) {
+                        p.out_i32[o] = x86_cvt_i32(roundf((float)a * p.sa * p.sb * p.inv_sc));
+                    } else if constexpr (EPI == kDequant) {
+                        p.out_f32[o] = (float)a * rmul * cmul[j];
+                    } else {
+                        epilogue_store<EPI>(p, m, n, a);
+                    }
+                }
+            });
+        });
+    });
+}
+
 // ------------------------------------ NT core GEMM, direct-to-LDS pipeline
 
 // gfx9 s_waitcnt immediate: vmcnt in bits [3:0] and [15:14], expcnt [6:4],
 // lgkmcnt [11:8]; a field at its maximum does not wait.
 constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8); }
 
+// Tuning knobs (defaults measured best on MI355X): LDS stages in the ring
+// and where the copies of a tile are issued (0: both operands in the first
+// half of an iteration, 1: both in the second half, 2: A in the first, B in
+// the second).
+#ifndef RPL_I8_STAGES
+#define RPL_I8_STAGES 4
+#endif
+#ifndef RPL_I8_DMA_SLOT
+#define RPL_I8_DMA_SLOT 2
+#endif
+// Big-tile kernel: 0 = one wave per SIMD (k_gemm_i8_nt_dma), 1 = 8-wave
+// ping-pong (k_gemm_i8_nt_pp), and the latter's LDS stages.
+#ifndef RPL_I8_BIG_KERNEL
+#define RPL_I8_BIG_KERNEL 0
+#endif
+#ifndef RPL_I8_PP_STAGES
+#define RPL_I8_PP_STAGES 4
+#endif
+
 namespace dma {
-constexpr int BM = 256, BN = 256, BK = 64, S = 4, kThreads = 256;
+constexpr int BM = 256, BN = 256, BK = 64, S = RPL_I8_STAGES, kThreads = 256;
+constexpr int kSlot = RPL_I8_DMA_SLOT;
+static_assert(S >= 3 && S * (BM + BN) * BK <= 160 * 1024, "LDS ring must fit 160 KB");
 constexpr int kTileBytes = BM * BK;          // one operand of one stage: 16 KB
 constexpr int kStageBytes = (BM + BN) * BK;  // 32 KB
 constexpr int kLoads = 4;                    // 1 KB loads per wave per operand per tile
@@ -506,16 +574,31 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
         voff_a[i] = (r < rows_a ? r : rows_a - 1) * lda + c;
         voff_b[i] = (r < rows_b ? r : rows_b - 1) * ldb + c;
     }
-    auto issue = [&](uint32_t kt, uint32_t stage) {
+    auto issue_a = [&](uint32_t kt, uint32_t stage) {
         int8_t* st = smem + stage * kStageBytes;
 #pragma unroll
         for (int i = 0; i < kLoads; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr)(st + (wave * 64 + i * 16) * BK), 16,
                                                      voff_a[i], kt * BK, 0, 0);
+    };
+    auto issue_b = [&](uint32_t kt, uint32_t stage) {
+        int8_t* st = smem + stage * kStageBytes;
 #pragma unroll
         for (int i = 0; i < kLoads; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr)(st + kTileBytes + (wave * 64 + i * 16) * BK),
                                                      16, voff_b[i], kt * BK, 0, 0);
+    };
+    auto issue = [&](uint32_t kt, uint32_t stage) {
+        issue_a(kt, stage);
+        issue_b(kt, stage);
+    };
+    // Wait until this wave's copies of tile kt+1 have landed, given that
+    // `later` whole tiles (plus `extra` single copies) were issued after it.
+    auto wait_after = [&](uint32_t later) {
+        static_for<S - 1>([&](auto C) {
+            constexpr int c = decltype(C)::value;
+            if (later == (uint32_t)c) __builtin_amdgcn_s_waitcnt(waitcnt_imm(c * kVmPerTile, 0));
+        });
     };
 
     // Fragment reads: lane feeds row lane%32 of each 32-row block with chunk
@@ -548,113 +631,223 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
     };
 
     const uint32_t nk = K / BK;
-    // Prologue: tiles 0..2 requested, tile 0 landed and visible.
-    issue(0, 0);
-    if (nk > 1) issue(1, 1);
-    if (nk > 2) issue(2, 2);
-    if (nk > 2)
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kVmPerTile, 0));
-    else
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+    // Prologue: tiles 0 .. S-2 requested, tile 0 landed and visible.
+    static_for<S - 1>([&](auto T) {
+        constexpr int t = decltype(T)::value;
+        if (t < nk) issue(t, t);
+    });
+    wait_after(nk - 1 < (uint32_t)(S - 2) ? nk - 1 : S - 2);  // tiles 1 .. min(S-2, nk-1) may stay in flight
     __builtin_amdgcn_s_barrier();
     F f0, f1;
     fload(0, 0, f0);
 
-    // Iteration kt: request tile kt+3 (into the stage tile kt-1 left), read
-    // tile kt's second half while multiplying its first, wait for tile kt+1
-    // and barrier, read tile kt+1's first half while multiplying kt's second.
+    // Iteration kt: request tile kt+S-1 (into the stage tile kt-1 left),
+    // read tile kt's second half while multiplying its first, wait for
+    // tile kt+1 and barrier, read tile kt+1's first half while multiplying
+    // kt's second.
     //
     // The steady state pins the instruction order (sched_group_barrier):
     // each fragment read is issued between two MFMAs early in the half, the
     // tile copies between the later MFMAs, so the MFMA pipe never waits on
     // an LDS read issued just before it (left alone, the scheduler sinks
     // every read to just before its first use and reuses its registers).
+    constexpr int kCopiesA = kSlot == 0 ? 2 * kLoads : kSlot == 2 ? kLoads : 0;
+    constexpr int kCopiesB = 2 * kLoads - kCopiesA;
+    // Copies issued after tile kt+1's at the barrier of iteration kt.
+    constexpr int kLaterSteady = (S - 3) * kVmPerTile + kCopiesA;
     uint32_t kt = 0;
-    for (; kt + S + 3 <= nk; kt += S) {
+    for (; kt + 2 * S - 1 <= nk; kt += S) {
         static_for<S>([&](auto U) {
             constexpr int u = decltype(U)::value;
             __builtin_amdgcn_sched_barrier(0);
-            issue(kt + u + 3, (u + 3) % S);
+            if constexpr (kSlot != 1) issue_a(kt + u + S - 1, (u + S - 1) % S);
+            if constexpr (kSlot == 0) issue_b(kt + u + S - 1, (u + S - 1) % S);
             fload(u, 1, f1);
             mma(f0);
             static_for<8>([&](auto) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
             });
-            static_for<8>([&](auto) {
+            static_for<kCopiesA>([&](auto) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // HBM -> LDS copy
             });
             __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kVmPerTile, 0));
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLaterSteady, 0));
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kSlot == 1) issue_a(kt + u + S - 1, (u + S - 1) % S);
+            if constexpr (kSlot != 0) issue_b(kt + u + S - 1, (u + S - 1) % S);
             fload((u + 1) % S, 0, f0);
             mma(f1);
             static_for<8>([&](auto) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
             });
-            static_for<8>([&](auto) { __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); });
+            static_for<kCopiesB>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // HBM -> LDS copy
+            });
             __builtin_amdgcn_sched_barrier(0);
         });
     }
+    // Last iterations: a whole tile is requested in the first half.
     for (; kt < nk; kt++) {
-        if (kt + 3 < nk) issue(kt + 3, (kt + 3) % S);
+        if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
         fload(kt % S, 1, f1);
         mma(f0);
-        if (kt + 3 < nk)
-            __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kVmPerTile, 0));
-        else if (kt + 3 == nk)
-            __builtin_amdgcn_s_waitcnt(waitcnt_imm(kVmPerTile, 0));
-        else
-            __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+        const uint32_t last = kt + S - 1 < nk - 1 ? kt + S - 1 : nk - 1;  // last tile requested so far
+        wait_after(last > kt + 1 ? last - kt - 1 : 0);
         __builtin_amdgcn_s_barrier();
         if (kt + 1 < nk) fload((kt + 1) % S, 0, f0);
         mma(f1);
     }
 
-    // Epilogue: result register r of lane l in block (i, j) is row
-    // 8*(r/4) + 4*(l/32) + r%4, column l%32.  Fully unrolled (the
-    // accumulators are only ever indexed by constants); values that depend
-    // on the column are loaded once per block column, those that depend on
-    // the row once per row; interior tiles skip the bounds checks.
-    const uint32_t mb = m0 + wm * 128 + 4 * (lane / 32), nb = n0 + wn * 128 + lane % 32;
-    const bool full = m0 + BM <= M && n0 + BN <= N;
-    int32_t cadd[4];  // kRaw: bias[n]
-    float cmul[4];    // kDequant: sw[n]
+    epilogue_tile<EPI, 4, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * 128 + lane % 32, M, N,
+                             m0 + BM <= M && n0 + BN <= N);
+}
+
+// --------------------------- NT core GEMM, 8-wave ping-pong (2 waves/SIMD)
+
+namespace pp {
+constexpr int BM = 256, BN = 256, BK = 64, kThreads = 512;
+constexpr int S = RPL_I8_PP_STAGES, D = S - 1;  // LDS stages; tiles requested ahead
+constexpr int kTileBytes = BM * BK, kStageBytes = (BM + BN) * BK;
+constexpr int kLoads = 4;  // 1 KB copies per wave per tile (its group's operand)
+static_assert(S >= 3 && S * kStageBytes <= 160 * 1024, "LDS ring must fit 160 KB");
+}  // namespace pp
+
+// 256 x 256 x 64 tiles, 8 waves: wave w runs on SIMD w%4 and belongs to
+// group g = w/4, so every SIMD hosts one wave of each group.  Each wave owns
+// a 128 x 64 block of the tile (4 x 2 MFMA blocks, 128 accumulators), so two
+// waves fit one SIMD.  The two groups alternate, one barrier apart:
+//
+//   phase 2t-1: group 0 reads its fragments of tile t;  group 1 multiplies tile t-1
+//   phase 2t  : group 0 multiplies tile t;            group 1 reads its fragments of tile t
+//
+// so on every SIMD one wave issues 16 back-to-back MFMAs while the other
+// issues its LDS reads and tile copies, and the roles swap at each barrier
+// with the next wave's operands already in registers.  A memory phase for
+// tile t also requests the wave's share of tile t+D (group 0 copies the A
+// tile, group 1 the B tile, each wave 4 x 1 KB) into the LDS stage that tile
+// t-1 left; each wave waits for its own copies of a tile before the barrier
+// that precedes the tile's first reads.  Copies, swizzle and row clamping as
+// in k_gemm_i8_nt_dma.
+template <int EPI>
+__global__ void __launch_bounds__(512, 1) k_gemm_i8_nt_pp(const int8_t* __restrict__ A, uint32_t lda,
+                                                          const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
+                                                          uint32_t N, uint32_t K, EpiParams p) {
+    using namespace pp;
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[S * kStageBytes];
+
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t grp = wave / 4, q = wave % 4;
+    const uint32_t wm = q % 2, wn = grp * 2 + q / 2;  // 128-row half, 64-column quarter
+    uint32_t im, in;
+    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, im, in);
+    const uint32_t m0 = im * BM, n0 = in * BN;
+    const uint32_t rows_a = M - m0 < (uint32_t)BM ? M - m0 : BM;
+    const uint32_t rows_b = N - n0 < (uint32_t)BN ? N - n0 : BN;
+
+    // This wave's copies: group 0 the A tile, group 1 the B tile; wave q of
+    // the group copies rows 64q .. 64q+63.
+    const uint32_t rows = grp ? rows_b : rows_a, ld = grp ? ldb : lda;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        grp ? uniform_rsrc(B + (uint64_t)n0 * ldb, rows_b * ldb) : uniform_rsrc(A + (uint64_t)m0 * lda, rows_a * lda);
+    uint32_t voff[kLoads];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t n = nb + j * 32;
-        cadd[j] = (EPI == kRaw && p.bias && n < N) ? (int32_t)p.bias[n] : 0;
-        cmul[j] = (EPI == kDequant && n < N) ? p.sw[p.sw_per_col ? n : 0] : 0.0f;
+    for (int i = 0; i < kLoads; i++) {
+        const uint32_t r = q * 64 + i * 16 + lane / 4;
+        voff[i] = (r < rows ? r : rows - 1) * ld + ((lane % 4) ^ swz(r)) * 16;
     }
-    static_for<4>([&](auto I) {
-        constexpr int i = decltype(I)::value;
-        static_for<16>([&](auto R) {
-            constexpr int r = decltype(R)::value;
-            const uint32_t m = mb + i * 32 + 8 * (r / 4) + r % 4;
-            const bool row_ok = full || m < M;
-            const float rmul = (EPI == kDequant && row_ok) ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
-            static_for<4>([&](auto J) {
-                constexpr int j = decltype(J)::value;
-                const uint32_t n = nb + j * 32;
-                if (full || (row_ok && n < N)) {
-                    const uint64_t o = (uint64_t)m * p.ldc + n;
-                    const int32_t a = acc[i][j][r];
-                    if constexpr (EPI == kRaw) {
-                        p.out_i32[o] = wrap_add(a, cadd[j]);
-                    } else if constexpr (EPI == kRequantPow2) {
-                        p.out_i32[o] = x86_cvt_i32(roundf((float)a * p.sa * p.sb * p.inv_sc));
-                    } else if constexpr (EPI == kDequant) {
-                        p.out_f32[o] = (float)a * rmul * cmul[j];
-                    } else {
-                        epilogue_store<EPI>(p, m, n, a);
-                    }
-                }
-            });
+    const uint32_t dst = grp * kTileBytes + q * 64 * BK;
+    auto issue = [&](uint32_t kt) {
+        int8_t* st = smem + (kt % S) * kStageBytes + dst;
+#pragma unroll
+        for (int i = 0; i < kLoads; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)(st + i * 16 * BK), 16, voff[i], kt * BK, 0, 0);
+    };
+    // Wait until this wave's copies of tile u have landed when `later` of
+    // its tile shares were requested after tile u's.
+    auto wait_later = [&](uint32_t later) {
+        static_for<D>([&](auto C) {
+            constexpr int c = decltype(C)::value;
+            if (later == (uint32_t)c) __builtin_amdgcn_s_waitcnt(waitcnt_imm(c * kLoads, 0));
         });
+    };
+
+    // Fragments of both 32-k steps of a tile: A blocks i (rows wm*128 +
+    // 32i + lane%32), B blocks j (rows wn*64 + 32j + lane%32), chunk
+    // 2kk + lane/32 at its swizzled slot (which depends on the lane only).
+    const uint32_t fr = lane % 32;
+    uint32_t foff[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) foff[kk] = fr * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
+    v4i fa[2][4], fb[2][2];
+    auto fread = [&](uint32_t kt) {
+        const int8_t* st = smem + (kt % S) * kStageBytes;
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                fa[kk][i] = *reinterpret_cast<const v4i*>(st + foff[kk] + (wm * 128 + i * 32) * BK);
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                fb[kk][j] = *reinterpret_cast<const v4i*>(st + kTileBytes + foff[kk] + (wn * 64 + j * 32) * BK);
+        }
+    };
+    v16i acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = (v16i){};
+    auto mma = [&]() {
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
+    };
+
+    const uint32_t nk = K / BK;
+    // Prologue: tiles 0 .. D-1 requested, tile 0 landed and visible.
+    static_for<D>([&](auto T) {
+        constexpr int t = decltype(T)::value;
+        if (t < nk) issue(t);
     });
+    wait_later(nk - 1 < (uint32_t)(D - 1) ? nk - 1 : D - 1);
+    __builtin_amdgcn_s_barrier();
+    if (grp == 1) __builtin_amdgcn_s_barrier();  // group 1 starts one phase later
+
+    for (uint32_t t = 0; t < nk; t++) {
+        // Memory phase: fragments of tile t, request tile t+D.
+        __builtin_amdgcn_sched_barrier(0);
+        fread(t);
+        if (t + D < nk) issue(t + D);
+        // Tile t+1 is first read right after the next barrier of group 1 /
+        // the one after of group 0; the wave that reaches it from this phase
+        // (group 1) waits for its copies here, group 0 after its MFMAs.
+        const uint32_t last = t + D < nk - 1 ? t + D : nk - 1;  // last tile requested so far
+        const uint32_t later = last > t + 1 ? last - t - 1 : 0;
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));          // own fragment reads complete
+        if (grp == 1) wait_later(later);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        // Compute phase: 16 MFMAs on the fragments in registers.
+        __builtin_amdgcn_sched_barrier(0);
+        mma();
+        __builtin_amdgcn_sched_barrier(0);
+        if (grp == 0) wait_later(later);
+        __builtin_amdgcn_s_barrier();
+    }
+    if (grp == 0) __builtin_amdgcn_s_barrier();  // group 0 ends one phase earlier
+
+    epilogue_tile<EPI, 4, 2>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * 64 + lane % 32, M, N,
+                             m0 + BM <= M && n0 + BN <= N);
 }
 
 // --------------------------------------------------- skinny (M <= 16) GEMM
@@ -940,8 +1133,12 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
     if (al && use_big_tile(M, N)) {
         if (K % dma::BK == 0 && (uint64_t)M * lda < (1ull << 31) && (uint64_t)N * ldb < (1ull << 31) && use_dma()) {
             const uint64_t tiles = (uint64_t)((M + dma::BM - 1) / dma::BM) * ((N + dma::BN - 1) / dma::BN);
-            hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI>), dim3((uint32_t)tiles), dim3(dma::kThreads), 0, s, A, lda, B,
-                               ldb, M, N, K, p);
+            if (RPL_I8_BIG_KERNEL == 1)
+                hipLaunchKernelGGL((k_gemm_i8_nt_pp<EPI>), dim3((uint32_t)tiles), dim3(pp::kThreads), 0, s, A, lda,
+                                   B, ldb, M, N, K, p);
+            else
+                hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI>), dim3((uint32_t)tiles), dim3(dma::kThreads), 0, s, A, lda,
+                                   B, ldb, M, N, K, p);
             return rplhip::check_launch("int8 GEMM");
         }
         return launch_nt<CfgBig, EPI>(A, lda, B, ldb, M, N, K, p, al, s);
