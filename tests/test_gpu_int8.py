@@ -260,3 +260,25 @@ def test_big_tile_int8_paths(gpu, orc, M, N, K):
     y = down(Y, np.float32, (M, N))
     assert bits_equal(y, (acc.astype(np.float32) * sx[:, None]) * sw[None, :])
     assert bits_equal(y[rows], orc.dequant_acc(acc[rows], sx[rows], True, sw, True))
+
+
+# Skinny GEMMs (M <= 16) on the LDS-staged MFMA kernel (k_skinny_dma): full K
+# slices with 4 waves (K = 8192) and 8 waves (K = 16384), partial slices
+# (K = 4096 + 64, 12288), ragged N; bit-exact against the oracle, int32 and
+# fused dequant.
+@pytest.mark.parametrize("M,K,N", [(5, 8192, 1000), (16, 8192, 77), (8, 16384, 300), (16, 12288, 129),
+                                   (12, 4160, 513), (16, 64, 40)])
+def test_skinny_mfma_vs_oracle(gpu, orc, M, K, N):
+    rng = np.random.default_rng(M * 31 + K + N)
+    x = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    b = rng.integers(-128, 128, N, dtype=np.int8)
+    say("skinny linear_int8", M, K, N)
+    ref = orc.linear_int8(x, w, None, M, K, N)
+    assert bits_equal(linear_int8(x, w, None, M, K, N), ref)
+    assert bits_equal(linear_int8(x, w, b, M, K, N), orc.linear_int8(x, w, b, M, K, N))
+    sx = (rng.random(M).astype(np.float32) + 0.5) * np.float32(0.01)
+    sw = (rng.random(N).astype(np.float32) + 0.5) * np.float32(0.02)
+    say("skinny linear_int8_dequant", M, K, N)
+    got = linear_int8_dequant(x, sx, True, w, sw, True, M, K, N)
+    assert bits_equal(got, orc.dequant_acc(ref, sx, True, sw, True))
