@@ -43,6 +43,28 @@ inline hipStream_t as_stream(rplhip_stream_t s) { return reinterpret_cast<hipStr
                                 hipGetErrorString(_e));                                 \
     } while (0)
 
+namespace rplhip {
+// Tile index -> (tile_m, tile_n) for a 1-D grid of tm x tn tiles:
+// 1. undo the round-robin XCD dispatch (block b runs on XCD b % 8) so that
+//    each XCD owns a contiguous range of virtual tile indices;
+// 2. walk that range in groups of kGroupM tile-rows, column by column.
+constexpr uint32_t kXcds = 8, kGroupM = 8;  // MI355X: 8 XCDs of 32 CUs
+
+__device__ __forceinline__ void tile_of(uint32_t b, uint32_t tm, uint32_t tn, uint32_t& im, uint32_t& in) {
+    const uint32_t T = tm * tn;
+    const uint32_t q = T / kXcds, r = T % kXcds;
+    const uint32_t x = b % kXcds, idx = b / kXcds;
+    const uint32_t t = x * q + (x < r ? x : r) + idx;
+    const uint32_t group = kGroupM * tn;
+    const uint32_t g = t / group, first = g * kGroupM;
+    const uint32_t gm = tm - first < kGroupM ? tm - first : kGroupM;
+    const uint32_t w = t - g * group;
+    im = first + w % gm;
+    in = w / gm;
+}
+
+}  // namespace rplhip
+
 // x86-64 cvttss2si: truncation toward zero; NaN and values outside
 // [-2^31, 2^31) give INT32_MIN.  The reference's (int32_t) casts of roundf
 // results compile to it, and its outcome is part of the observable contract

@@ -16,6 +16,10 @@
 // consecutive columns, so C is read and written with 128-bit accesses.
 #include "common.h"
 
+#ifndef RPL_F32_XCD
+#define RPL_F32_XCD 1
+#endif
+
 namespace {
 
 constexpr int BM = 128, BN = 128, BK = 32;
@@ -132,7 +136,15 @@ __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, u
     const OpB opb{B, ldb, N, K};
     const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
     const uint32_t wm = (wave / 2) * TM, wn = (wave % 2) * TN;
+#if RPL_F32_XCD
+    // 1-D grid in the XCD-aware grouped tile order (A and B panels shared by
+    // the CUs of an XCD stay in its L2).
+    uint32_t im, in;
+    rplhip::tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, im, in);
+    const uint32_t m0 = im * BM, n0 = in * BN;
+#else
     const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+#endif
 
     v4f acc[FM][FN];
 #pragma unroll
@@ -224,8 +236,14 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
     // multiples of 4 floats and 16-byte aligned bases.
     bool vec = aligned16(A) && aligned16(B) && aligned16(C) && lda % 4 == 0 && ldb % 4 == 0 &&
                ldc % 4 == 0 && N % 4 == 0 && (TA ? M % 4 == 0 : K % 4 == 0) && (TB ? K % 4 == 0 : true);
+#if RPL_F32_XCD
+    const uint64_t tiles = (uint64_t)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
+    if (tiles > 0x7fffffffull) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "sgemm: %u x %u too large", M, N);
+    dim3 grid((uint32_t)tiles);
+#else
     dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
     if (grid.y > 65535) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "sgemm: M=%u too large", M);
+#endif
     if (vec)
         hipLaunchKernelGGL((k_sgemm<TA, TB, true>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B, ldb,
                            beta, C, ldc);

@@ -45,6 +45,8 @@
 
 namespace {
 
+using rplhip::tile_of;
+
 // Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 at compile time.
 template <int N, int I = 0, class F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -131,25 +133,6 @@ __device__ __forceinline__ v4i load_chunk_stream(const int8_t* __restrict__ base
     if (ALIGNED && r < rows && k < K)
         return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(base + (uint64_t)r * ld + k));
     return load_chunk<ALIGNED>(base, ld, rows, K, r, k);
-}
-
-// Tile index -> (tile_m, tile_n) for a 1-D grid of tm x tn tiles:
-// 1. undo the round-robin XCD dispatch (block b runs on XCD b % 8) so that
-//    each XCD owns a contiguous range of virtual tile indices;
-// 2. walk that range in groups of kGroupM tile-rows, column by column.
-constexpr uint32_t kXcds = 8, kGroupM = 8;
-
-__device__ __forceinline__ void tile_of(uint32_t b, uint32_t tm, uint32_t tn, uint32_t& im, uint32_t& in) {
-    const uint32_t T = tm * tn;
-    const uint32_t q = T / kXcds, r = T % kXcds;
-    const uint32_t x = b % kXcds, idx = b / kXcds;
-    const uint32_t t = x * q + (x < r ? x : r) + idx;
-    const uint32_t group = kGroupM * tn;
-    const uint32_t g = t / group, first = g * kGroupM;
-    const uint32_t gm = tm - first < kGroupM ? tm - first : kGroupM;
-    const uint32_t w = t - g * group;
-    im = first + w % gm;
-    in = w / gm;
 }
 
 // ------------------------------------------------------------ NT core GEMM

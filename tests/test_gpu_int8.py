@@ -220,8 +220,10 @@ def _requant_f32(acc, sa, sb, sc):
 
 # Shapes with >= 2 tiles of 256 x 256 per CU take the direct-to-LDS kernel
 # (k_gemm_i8_nt_dma); K = 448 and 832 run its steady-state loop and tails of
-# 3 and 5 tiles; the first shape has ragged edges in M and N.
-BIG = [(5890, 5900, 832), (6144, 6144, 448)]
+# 3 and 5 tiles.  gemm_int8 reads B [K,N] in place (transposed LDS reads)
+# when N % 16 == 0 (5888, 6144) and transposes it first otherwise (5900);
+# the first two shapes have ragged edges in M and N.
+BIG = [(5890, 5900, 832), (5890, 5888, 832), (6144, 6144, 448)]
 
 
 @pytest.mark.parametrize("M,N,K", BIG)
@@ -251,6 +253,24 @@ def test_big_tile_int8_paths(gpu, orc, M, N, K):
         assert bits_equal(got, _requant_f32(acc, sa, sb, sc))
         ref = orc.gemm_int8(np.ascontiguousarray(A[rows]), B, len(rows), N, K, sa, sb, sc)
         assert bits_equal(got[rows], ref)
+    # Zero point on A's side only (zb): acc - zb * rowsum(A), generic requant.
+    zb = -7
+    out = empty((M, N), np.int32)
+    say("big-tile gemm_int8 zb", M, N, K)
+    rpl_amd.check(lib.rplhip_gemm_int8(dA.ptr, dB.ptr, out.ptr, M, N, K, 0.013, 0.7, 0.25, 0, zb, None))
+    got = down(out, np.int32, (M, N))
+    rs = A.astype(np.int64).sum(1)
+    acc_zb = (acc.astype(np.int64) - zb * rs[:, None]).astype(np.int32)
+    assert bits_equal(got, _requant_f32(acc_zb, 0.013, 0.7, 0.25))
+    assert bits_equal(got[rows], orc.gemm_int8(np.ascontiguousarray(A[rows]), B, len(rows), N, K, 0.013, 0.7, 0.25,
+                                               0, zb))
+    # gemm_int8_dequant: per-tensor A scale, per-column B scale, B [K,N].
+    sa1 = np.float32([0.02])
+    sbc = (rng.random(N).astype(np.float32) + 0.5) * np.float32(0.03)
+    dsa1, dsbc, Yd = up(sa1), up(sbc), empty((M, N), np.float32)
+    say("big-tile gemm_int8_dequant", M, N, K)
+    rpl_amd.check(lib.rplhip_gemm_int8_dequant(dA.ptr, dsa1.ptr, 0, dB.ptr, dsbc.ptr, 1, Yd.ptr, M, N, K, None))
+    assert bits_equal(down(Yd, np.float32, (M, N)), (acc.astype(np.float32) * sa1[0]) * sbc[None, :])
     # linear_int8_dequant: per-row x scales, per-column w scales, fp32 out.
     sx = (rng.random(M).astype(np.float32) + 0.5) * np.float32(0.01)
     sw = (rng.random(N).astype(np.float32) + 0.5) * np.float32(0.02)
