@@ -80,6 +80,157 @@ def cpu_baseline_int8(n, rows, qa, qb):
     return 2.0 * rows * n * n / dt / 1e12, dt
 
 
+def _tensor(lib, arr, requires_grad=False):
+    arr = np.ascontiguousarray(arr, np.float32)
+    shape = (C.c_uint32 * arr.ndim)(*arr.shape)
+    t = lib.tensor_create(arr.ndim, shape, requires_grad)
+    C.memmove(t.contents.data, arr.ctypes.data, arr.nbytes)
+    return t
+
+
+def _cpu_ms(fn, reps=1):
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) * 1e3 / reps
+
+
+def bench_configs(lib, stream, timer, steps, with_cpu):
+    """BASELINE configs 0-3 on the device (inputs resident, HIP events on one
+    stream), each with the oracle (the reference's CPU path restated, same
+    flags, all host cores) timed on the same inputs or a stated row sample."""
+    from oracle import Oracle
+
+    orc = Oracle() if with_cpu else None
+    out = {}
+    sync = lambda: check(lib.rplhip_stream_synchronize(stream))  # noqa: E731
+
+    # cfg 0: FP32 512^3 NN, U[-1,1]
+    n = 512
+    A = rpl_amd.fill_uniform(n * n, seed(0, 0)).reshape(n, n)
+    B = rpl_amd.fill_uniform(n * n, seed(0, 1)).reshape(n, n)
+    dA, dB, dC = DeviceBuffer.from_array(A), DeviceBuffer.from_array(B), DeviceBuffer(n * n * 4)
+    f = lambda: check(lib.rplhip_sgemm(0, 0, n, n, n, 1.0, dA.ptr, n, dB.ptr, n, 0.0, dC.ptr, n, stream))  # noqa
+    ms, _ = timer.time(f, steps * 5, 5)
+    e = {"us": round(ms * 1e3, 2), "TFLOP/s": round(2 * n ** 3 / (ms * 1e-3) / 1e12, 2)}
+    if orc:
+        c = _cpu_ms(lambda: orc.sgemm(A, B, np.zeros((n, n), np.float32), n, n, n))
+        e["cpu_ms"] = round(c, 2)
+    out["cfg0_fp32_512"] = e
+
+    # cfg 1: INT8 512^3: N(0,1) -> per-tensor symmetric quantize (both) ->
+    # i8 GEMM with the fused fp32 dequant (scale_A * scale_B); a step is the
+    # two quantizations and the GEMM.
+    A = rpl_amd.fill_normal(n * n, seed(1, 0))
+    B = rpl_amd.fill_normal(n * n, seed(1, 1))
+    dA, dB = DeviceBuffer.from_array(A), DeviceBuffer.from_array(B)
+    qA, qB, sA, sB = DeviceBuffer(n * n), DeviceBuffer(n * n), DeviceBuffer(4), DeviceBuffer(4)
+    dY = DeviceBuffer(n * n * 4)
+
+    def cfg1():
+        check(lib.rplhip_quantize_symmetric(dA.ptr, n * n, qA.ptr, sA.ptr, stream))
+        check(lib.rplhip_quantize_symmetric(dB.ptr, n * n, qB.ptr, sB.ptr, stream))
+        check(lib.rplhip_gemm_int8_dequant(qA.ptr, sA.ptr, 0, qB.ptr, sB.ptr, 0, dY.ptr, n, n, n, stream))
+
+    ms, _ = timer.time(cfg1, steps * 5, 5)
+    e = {"us": round(ms * 1e3, 2), "TOP/s_incl_quantize": round(2 * n ** 3 / (ms * 1e-3) / 1e12, 2)}
+    if orc:
+        def cpu1():
+            qa, sa = orc.quantize_symmetric(A)
+            qb, sb = orc.quantize_symmetric(B)
+            orc.gemm_int8(qa.reshape(n, n), qb.reshape(n, n), n, n, n)
+        e["cpu_ms"] = round(_cpu_ms(cpu1), 2)
+    out["cfg1_int8_512"] = e
+
+    # cfg 2: MLP 784 -> 128 (ReLU) -> 10 training step at batch 4096 through
+    # include/rpl.h (linear_forward, tensor_relu, tensor_mse_loss,
+    # tensor_backward), every tensor GPU-resident; a step also zeroes the
+    # parameter gradients and frees the step's tensors.
+    Bt, IN, H, O = 4096, 784, 128, 10
+    X = rpl_amd.fill_uniform(Bt * IN, seed(2, 0), 0.0, 1.0).reshape(Bt, IN)
+    _, Y = rpl_amd.fill_labels(Bt, seed(2, 1), O)
+    W1 = rpl_amd.fill_uniform(H * IN, seed(2, 2), -np.sqrt(6 / IN), np.sqrt(6 / IN)).reshape(H, IN)
+    W2 = rpl_amd.fill_uniform(O * H, seed(2, 3), -np.sqrt(6 / H), np.sqrt(6 / H)).reshape(O, H)
+    l1, l2 = lib.linear_create(IN, H), lib.linear_create(H, O)
+    for layer, W in ((l1, W1), (l2, W2)):
+        C.memmove(layer.contents.weight.contents.data, W.ctypes.data, W.nbytes)
+        lib.tensor_fill(layer.contents.bias, 0.0)
+        lib.tensor_to_gpu(layer.contents.weight)
+        lib.tensor_to_gpu(layer.contents.bias)
+    tX, tY = _tensor(lib, X), _tensor(lib, Y)
+    lib.tensor_to_gpu(tX)
+    lib.tensor_to_gpu(tY)
+    params = (l1.contents.weight, l1.contents.bias, l2.contents.weight, l2.contents.bias)
+
+    def cfg2():
+        for t in params:
+            lib.tensor_zero_grad(t)
+        h = lib.linear_forward(l1, tX)
+        a = lib.tensor_relu(h)
+        o = lib.linear_forward(l2, a)
+        loss = lib.tensor_mse_loss(o, tY)
+        lib.tensor_backward(loss)
+        for t in (loss, o, a, h):
+            lib.tensor_free(t)
+
+    for _ in range(3):
+        cfg2()
+    lib.rpl_gpu_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        cfg2()
+    lib.rpl_gpu_synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    err = lib.rpl_last_error()
+    flop = 1_675_624_448
+    e = {"us": round(ms * 1e3, 1), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 3), "timing": "host clock, synced",
+         "error": err.decode() if err else None}
+    if orc:
+        b = np.zeros(H, np.float32), np.zeros(O, np.float32)
+        e["cpu_ms"] = round(_cpu_ms(lambda: orc.mlp_step(X, Y, W1, b[0], W2, b[1])), 1)
+    out["cfg2_mlp_step_b4096"] = e
+    for layer in (l1, l2):
+        lib.linear_free(layer)
+    lib.tensor_free(tX)
+    lib.tensor_free(tY)
+
+    # cfg 3: INT8 linear layers, M=2048 tokens, K=4096, N in {4096, 11008}:
+    # X N(0,1) quantized per token on the device each step, W N(0,0.02)
+    # quantized per output channel once (weights), fused fp32 dequant.
+    M, K = 2048, 4096
+    X = rpl_amd.fill_normal(M * K, seed(3, 0)).reshape(M, K)
+    dX, qX, sX = DeviceBuffer.from_array(X), DeviceBuffer(M * K), DeviceBuffer(M * 4)
+    for N in (4096, 11008):
+        W = rpl_amd.fill_normal(N * K, seed(3, 1), 0.0, 0.02).reshape(N, K)
+        dW, qW, sW = DeviceBuffer.from_array(W), DeviceBuffer(N * K), DeviceBuffer(N * 4)
+        check(lib.rplhip_quantize_per_channel(dW.ptr, N, K, qW.ptr, sW.ptr, stream))
+        dY = DeviceBuffer(M * N * 4)
+        gemm = lambda: check(lib.rplhip_linear_int8_dequant(qX.ptr, sX.ptr, 1, qW.ptr, sW.ptr, 1, dY.ptr, M, K, N,  # noqa
+                                                            stream))
+        check(lib.rplhip_quantize_per_channel(dX.ptr, M, K, qX.ptr, sX.ptr, stream))
+        ms_g, _ = timer.time(gemm, steps * 2, 3)
+
+        def step():
+            check(lib.rplhip_quantize_per_channel(dX.ptr, M, K, qX.ptr, sX.ptr, stream))
+            gemm()
+
+        ms_s, _ = timer.time(step, steps * 2, 3)
+        ops = 2.0 * M * N * K
+        e = {"gemm_us": round(ms_g * 1e3, 2), "gemm_TOP/s": round(ops / (ms_g * 1e-3) / 1e12, 1),
+             "step_us_incl_x_quantize": round(ms_s * 1e3, 2)}
+        if orc:
+            rows = 128
+            sync()
+            qx = qX.to_array(np.int8, (M, K))[:rows]
+            qw = qW.to_array(np.int8, (N, K))
+            c = _cpu_ms(lambda: orc.linear_int8(qx, qw, None, rows, K, N))
+            e["cpu_TOP/s"] = round(2.0 * rows * N * K / (c * 1e-3) / 1e12, 4)
+            e["cpu_sample"] = f"linear_int8 oracle on {rows} of {M} rows"
+        out[f"cfg3_linear_int8_N{N}"] = e
+        del dW, qW, sW, dY
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -88,7 +239,7 @@ def main():
     ap.add_argument("--n", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=512)
-    ap.add_argument("--only", choices=["int8", "int8-kernel", "fp32", "skinny"],
+    ap.add_argument("--only", choices=["int8", "int8-kernel", "fp32", "skinny", "configs"],
                     help="run one leg only (for profiling); the JSON line then has nulls for the rest")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -177,6 +328,11 @@ def main():
                                "frac_hbm": round(byts / (ms_s * 1e-3) / 1e9 / PEAK_HBM_GBS, 3)}
         del Ws
 
+    configs = None
+    if n == 8192 and want("configs"):
+        log("bench: configs 0-3")
+        configs = bench_configs(lib, stream, timer, max(args.steps // 2, 5), not args.no_cpu)
+
     cpu = None
     if not args.no_cpu and args.only is None:
         log(f"bench: cpu baseline (oracle, {args.cpu_rows}-row slab)")
@@ -219,6 +375,7 @@ def main():
         "roofline_fp32": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4), "kernel": "k_sgemm"},
         "skinny_int8": skinny,
+        "configs": configs,
         "cpu_baseline": cpu,
         "device": {"arch": arch.value.decode(), "cus": cus.value, "clock_mhz": clk.value // 1000},
         "wall_s": {"int8": round(wall_i8, 3), "fp32": round(wall_f32, 3)},

@@ -16,10 +16,6 @@
 // consecutive columns, so C is read and written with 128-bit accesses.
 #include "common.h"
 
-#ifndef RPL_F32_XCD
-#define RPL_F32_XCD 1
-#endif
-
 namespace {
 
 constexpr int BM = 128, BN = 128, BK = 32;
@@ -122,11 +118,15 @@ struct Operand {
     }
 };
 
-template <bool TA, bool TB, bool VEC>
+// SPLIT: block (tile, blockIdx.y) multiplies only k in [blockIdx.y * kps,
+// +kps) (kps a multiple of BK) and stores the raw partial tile to
+// C + blockIdx.y * M * ldc (a workspace; alpha, beta are applied by
+// k_splitk_reduce).
+template <bool TA, bool TB, bool VEC, bool SPLIT>
 __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, uint32_t K, float alpha,
                                                        const float* __restrict__ A, uint32_t lda,
                                                        const float* __restrict__ B, uint32_t ldb, float beta,
-                                                       float* __restrict__ C, uint32_t ldc) {
+                                                       float* __restrict__ C, uint32_t ldc, uint32_t kps) {
     using OpA = Operand<!TA, VEC>;
     using OpB = Operand<TB, VEC>;
     __shared__ __attribute__((aligned(16))) float As[2][kTileFloats];
@@ -136,15 +136,11 @@ __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, u
     const OpB opb{B, ldb, N, K};
     const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
     const uint32_t wm = (wave / 2) * TM, wn = (wave % 2) * TN;
-#if RPL_F32_XCD
-    // 1-D grid in the XCD-aware grouped tile order (A and B panels shared by
-    // the CUs of an XCD stay in its L2).
+    // 1-D tile grid in the XCD-aware grouped order (A and B panels shared
+    // by the CUs of an XCD stay in its L2).
     uint32_t im, in;
     rplhip::tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, im, in);
     const uint32_t m0 = im * BM, n0 = in * BN;
-#else
-    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-#endif
 
     v4f acc[FM][FN];
 #pragma unroll
@@ -166,13 +162,16 @@ __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, u
         for (int i = 0; i < kLoads; i++) OpB::store(Bs[buf], tid + i * kThreads, rb[i]);
     };
 
-    const uint32_t nk = (K + BK - 1) / BK;
-    gload(0);
+    const uint32_t kbeg = SPLIT ? blockIdx.y * kps : 0;
+    const uint32_t kend = SPLIT && kbeg + kps < K ? kbeg + kps : K;
+    if (SPLIT) C += (uint64_t)blockIdx.y * M * ldc;
+    const uint32_t nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    gload(kbeg);
     sstore(0);
     __syncthreads();
     for (uint32_t kt = 0; kt < nk; kt++) {
         const int buf = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * BK);
+        if (kt + 1 < nk) gload(kbeg + (kt + 1) * BK);
 #pragma unroll
         for (int kh = 0; kh < BK / 16; kh++) {
             float fa[4][4], fb[4][4];
@@ -192,7 +191,18 @@ __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, u
 
     // Epilogue: lane owns column lane%16 and rows 4*(lane/16)+r of each block.
     const uint32_t li = lane % 16, rg = 4 * (lane / 16);
-    if (!TB && VEC) {
+    if (SPLIT) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    uint32_t m = m0 + OpA::row_of(wm, i, rg + r);
+                    uint32_t n = n0 + OpB::row_of(wn, j, li);
+                    if (m < M && n < N) C[(uint64_t)m * ldc + n] = acc[i][j][r];
+                }
+    } else if (!TB && VEC) {
         // Interleaved columns: block j holds column li*4 + j -> 4 consecutive
         // columns per lane, one float4 read-modify-write per (i, r).
 #pragma unroll
@@ -227,7 +237,34 @@ __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, u
     }
 }
 
+// C = alpha * sum_s W[s] + beta * C over the split partials W[s] ([M, N],
+// ld N), summed in split order (deterministic).
+__global__ void __launch_bounds__(256) k_splitk_reduce(const float* __restrict__ W, uint32_t splits, uint32_t M,
+                                                       uint32_t N, float alpha, float beta, float* __restrict__ C,
+                                                       uint32_t ldc) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (uint64_t)M * N) return;
+    const uint32_t m = (uint32_t)(i / N), n = (uint32_t)(i % N);
+    float sum = W[i];
+    for (uint32_t s = 1; s < splits; s++) sum += W[(uint64_t)s * M * N + i];
+    float* cp = &C[(uint64_t)m * ldc + n];
+    *cp = alpha * sum + beta * *cp;
+}
+
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
+
+// K splits for a grid of `tiles` tiles: enough blocks to fill the CUs twice,
+// each split at least kMinKSplit long (a multiple of BK); 1 = no split.
+#ifndef RPL_F32_MIN_KSPLIT
+#define RPL_F32_MIN_KSPLIT 256
+#endif
+uint32_t k_splits(uint64_t tiles, uint32_t K) {
+    const uint64_t want = 2ull * rplhip::cu_count();
+    if (tiles >= want / 2 || K < 2 * RPL_F32_MIN_KSPLIT) return 1;
+    uint64_t s = (want + tiles - 1) / tiles;
+    const uint64_t cap = K / RPL_F32_MIN_KSPLIT;
+    return (uint32_t)(s < cap ? s : cap);
+}
 
 template <bool TA, bool TB>
 int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint32_t lda, const float* B,
@@ -236,20 +273,42 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
     // multiples of 4 floats and 16-byte aligned bases.
     bool vec = aligned16(A) && aligned16(B) && aligned16(C) && lda % 4 == 0 && ldb % 4 == 0 &&
                ldc % 4 == 0 && N % 4 == 0 && (TA ? M % 4 == 0 : K % 4 == 0) && (TB ? K % 4 == 0 : true);
-#if RPL_F32_XCD
     const uint64_t tiles = (uint64_t)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
     if (tiles > 0x7fffffffull) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "sgemm: %u x %u too large", M, N);
     dim3 grid((uint32_t)tiles);
-#else
-    dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-    if (grid.y > 65535) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "sgemm: M=%u too large", M);
-#endif
+    const uint32_t splits = k_splits(tiles, K);
+    if (splits > 1) {
+        // Partial tiles into a stream-ordered workspace, then one reduction.
+        uint32_t kps = (K + splits - 1) / splits;
+        kps = (kps + BK - 1) / BK * BK;
+        const uint32_t ns = (K + kps - 1) / kps;
+        void* ws = nullptr;
+        int st = rplhip::ws_alloc(&ws, (size_t)ns * M * N * sizeof(float), s);
+        if (st) return st;
+        dim3 g2(grid.x, ns);
+        float* W = (float*)ws;
+        if (vec)
+            hipLaunchKernelGGL((k_sgemm<TA, TB, true, true>), g2, dim3(kThreads), 0, s, M, N, K, 1.0f, A, lda, B,
+                               ldb, 0.0f, W, N, kps);
+        else
+            hipLaunchKernelGGL((k_sgemm<TA, TB, false, true>), g2, dim3(kThreads), 0, s, M, N, K, 1.0f, A, lda, B,
+                               ldb, 0.0f, W, N, kps);
+        st = rplhip::check_launch("sgemm (split-K)");
+        if (!st) {
+            const uint64_t total = (uint64_t)M * N;
+            hipLaunchKernelGGL(k_splitk_reduce, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, W, ns, M, N,
+                               alpha, beta, C, ldc);
+            st = rplhip::check_launch("sgemm (split-K reduction)");
+        }
+        rplhip::ws_free(ws, s);
+        return st;
+    }
     if (vec)
-        hipLaunchKernelGGL((k_sgemm<TA, TB, true>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B, ldb,
-                           beta, C, ldc);
+        hipLaunchKernelGGL((k_sgemm<TA, TB, true, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B,
+                           ldb, beta, C, ldc, K);
     else
-        hipLaunchKernelGGL((k_sgemm<TA, TB, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B, ldb,
-                           beta, C, ldc);
+        hipLaunchKernelGGL((k_sgemm<TA, TB, false, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B,
+                           ldb, beta, C, ldc, K);
     return rplhip::check_launch("sgemm");
 }
 

@@ -37,9 +37,11 @@ void tensor_add_out(Tensor* out, const Tensor* a, const Tensor* b) {
 
 /* src/rpl_core.c:131-135 */
 Tensor* tensor_add(const Tensor* a, const Tensor* b) {
-    Tensor* out = tensor_create(a->dims, a->shape, a->requires_grad || b->requires_grad);
+    const int gpu = any_gpu(a, b);
+    Tensor* out = (gpu ? rpl__tensor_create_gpu : tensor_create)(a->dims, a->shape,
+                                                                 a->requires_grad || b->requires_grad);
     if (!out) return NULL;
-    if (any_gpu(a, b) && !rpl__attach(out, 0)) return out;
+    if (gpu && !rpl__attach(out, 0)) return out;
     tensor_add_out(out, a, b);
     return out;
 }
@@ -53,9 +55,10 @@ void tensor_add_gpu(Tensor* out, const Tensor* a, const Tensor* b) {
 
 /* src/rpl_core.c:274-300 */
 Tensor* tensor_relu(const Tensor* t) {
-    Tensor* out = tensor_create(t->dims, t->shape, t->requires_grad);
+    const int gpu = rpl__is_gpu(t);
+    Tensor* out = (gpu ? rpl__tensor_create_gpu : tensor_create)(t->dims, t->shape, t->requires_grad);
     if (!out) return NULL;
-    if (rpl__is_gpu(t) && !rpl__attach(out, 0)) return out;
+    if (gpu && !rpl__attach(out, 0)) return out;
     if (!rpl_gpu_init()) return out;
     RplStage s = {0};
     const float* dx = rpl__view_data(&s, t, 1, 0);
@@ -237,11 +240,17 @@ Linear* linear_create(uint32_t in_features, uint32_t out_features) {
  * broadcast bias add; matmul_out stays alive as part of the graph. */
 Tensor* linear_forward(Linear* layer, const Tensor* input) {
     uint32_t output_shape[2] = {input->shape[0], layer->out_features};
-    Tensor* matmul_out = tensor_create(2, output_shape, input->requires_grad || layer->weight->requires_grad);
+    const int gpu = any_gpu(input, layer->weight) || rpl__is_gpu(layer->bias);
+    Tensor* (*create)(uint32_t, const uint32_t*, bool) = gpu ? rpl__tensor_create_gpu : tensor_create;
+    Tensor* matmul_out = create(2, output_shape, input->requires_grad || layer->weight->requires_grad);
     if (!matmul_out) return NULL;
-    int gpu = any_gpu(input, layer->weight) || rpl__is_gpu(layer->bias);
     if (gpu && !rpl__attach(matmul_out, 0)) return NULL;
-    tensor_fill(matmul_out, 0.0f);
+    /* Zero the buffer the GEMM reads as C (beta = 0 still reads it): on the
+     * device only when resident (its host copy is stale by definition). */
+    if (gpu)
+        rpl__ok(rplhip_fill(rpl__dev_data(matmul_out), matmul_out->size, 0.0f, NULL), "linear_forward");
+    else
+        tensor_fill(matmul_out, 0.0f);
     tensor_gemm(matmul_out, input, layer->weight, 1.0f, 0.0f, false, true);
     if (matmul_out->requires_grad) {
         matmul_out->parent1 = (Tensor*)input;
@@ -249,10 +258,11 @@ Tensor* linear_forward(Linear* layer, const Tensor* input) {
         matmul_out->backward_fn = backward_matmul;
         matmul_out->is_leaf = false;
     }
-    Tensor* out = tensor_create(2, output_shape, matmul_out->requires_grad || layer->bias->requires_grad);
+    Tensor* out = create(2, output_shape, matmul_out->requires_grad || layer->bias->requires_grad);
     if (!out) return NULL;
     if (gpu && !rpl__attach(out, 0)) return NULL;
     tensor_add_out(out, matmul_out, layer->bias);
+    if (gpu) rpl__adopt(out, matmul_out);
     return out;
 }
 

@@ -42,10 +42,16 @@ Tensor* tensor_matmul(const Tensor* a, const Tensor* b) {
     uint32_t M = a->shape[a->dims - 2];
     uint32_t N = b->shape[b->dims - 1];
     uint32_t shape[2] = {M, N};
-    Tensor* out = tensor_create(2, shape, a->requires_grad || b->requires_grad);
+    const int gpu = rpl__is_gpu(a) || rpl__is_gpu(b);
+    Tensor* out = (gpu ? rpl__tensor_create_gpu : tensor_create)(2, shape, a->requires_grad || b->requires_grad);
     if (!out) return NULL;
-    if ((rpl__is_gpu(a) || rpl__is_gpu(b)) && !rpl__attach(out, 0)) return out;
-    tensor_fill(out, 0.0f);
+    if (gpu && !rpl__attach(out, 0)) return out;
+    /* Zero C (the GEMM reads it even with beta = 0): on the device only when
+     * resident, the host copy being stale until tensor_from_gpu. */
+    if (gpu)
+        rpl__ok(rplhip_fill(rpl__dev_data(out), out->size, 0.0f, NULL), "tensor_matmul");
+    else
+        tensor_fill(out, 0.0f);
     tensor_gemm(out, a, b, 1.0f, 0.0f, false, false);
     if (out->requires_grad) {
         out->parent1 = (Tensor*)a;

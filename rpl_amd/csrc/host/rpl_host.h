@@ -28,6 +28,12 @@ float* rpl__dev_grad(const Tensor* t);
  * t->grad is set); copy the host values up when `upload`.  Returns 1 on
  * success. */
 int rpl__attach(Tensor* t, int upload);
+/* tensor_create for an output that becomes GPU-resident at once (host
+ * gradient left unzeroed: stale while resident). */
+Tensor* rpl__tensor_create_gpu(uint32_t dims, const uint32_t* shape, bool requires_grad);
+/* Release internal's device buffers when owner is freed (internal is a
+ * graph tensor nothing else references, e.g. linear_forward's GEMM output). */
+void rpl__adopt(const Tensor* owner, Tensor* internal);
 int rpl__is_gpu(const Tensor* t);
 /* Give a GPU-resident tensor a zeroed device gradient if it has none (a
  * root whose host gradient was created after it went to the device). */

@@ -293,8 +293,22 @@ void* rpitorch_aligned_alloc(size_t alignment, size_t size) {
 
 void rpitorch_aligned_free(void* ptr) { free(ptr); }
 
+static Tensor* tensor_create_impl(uint32_t dims, const uint32_t* shape, bool requires_grad, int zero_grad);
+
 /* src/rpl_core.c:43-70 */
 Tensor* tensor_create(uint32_t dims, const uint32_t* shape, bool requires_grad) {
+    return tensor_create_impl(dims, shape, requires_grad, 1);
+}
+
+/* An op's output that is about to become GPU-resident: the host buffers are
+ * allocated (tensor_from_gpu fills them) but the host gradient is not
+ * zeroed -- while a tensor is GPU-resident its host copies are stale by
+ * definition, and its device gradient is zeroed by rpl__attach. */
+Tensor* rpl__tensor_create_gpu(uint32_t dims, const uint32_t* shape, bool requires_grad) {
+    return tensor_create_impl(dims, shape, requires_grad, 0);
+}
+
+static Tensor* tensor_create_impl(uint32_t dims, const uint32_t* shape, bool requires_grad, int zero_grad) {
     Tensor* t = (Tensor*)calloc(1, sizeof(Tensor));
     if (!t) return NULL;
     if (dims > MAX_DIMS) {
@@ -318,17 +332,70 @@ Tensor* tensor_create(uint32_t dims, const uint32_t* shape, bool requires_grad) 
     t->data = (float*)t->_allocation;
     if (requires_grad) {
         t->grad = (float*)rpitorch_aligned_alloc(64, bytes);
-        if (t->grad) memset(t->grad, 0, bytes);
+        if (t->grad && zero_grad) memset(t->grad, 0, bytes);
     }
     t->requires_grad = requires_grad;
     t->is_leaf = true;
     return t;
 }
 
+/* ------------------------------------------- internal graph tensors */
+
+/* linear_forward's intermediate GEMM output is never freed by the reference
+ * (src/rpl_nn.c:73-74): only the returned tensor points at it.  Its host
+ * memory leaks as there; its device buffers are released when the tensor
+ * that owns it is freed, so a training loop does not grow device memory. */
+typedef struct {
+    const Tensor* owner;
+    Tensor* internal;
+} Adopted;
+
+static pthread_mutex_t g_adopt_mu = PTHREAD_MUTEX_INITIALIZER;
+static Adopted* g_adopt;
+static size_t g_adopt_len, g_adopt_cap;
+
+void rpl__adopt(const Tensor* owner, Tensor* internal) {
+    if (!owner || !internal || !rpl__is_gpu(internal)) return;
+    pthread_mutex_lock(&g_adopt_mu);
+    if (g_adopt_len == g_adopt_cap) {
+        size_t nc = g_adopt_cap ? 2 * g_adopt_cap : 64;
+        Adopted* na = (Adopted*)realloc(g_adopt, nc * sizeof(Adopted));
+        if (!na) {
+            pthread_mutex_unlock(&g_adopt_mu);
+            return; /* keeps the device buffers, like the host ones */
+        }
+        g_adopt = na;
+        g_adopt_cap = nc;
+    }
+    g_adopt[g_adopt_len].owner = owner;
+    g_adopt[g_adopt_len].internal = internal;
+    g_adopt_len++;
+    pthread_mutex_unlock(&g_adopt_mu);
+}
+
+static void release_adopted(const Tensor* owner) {
+    pthread_mutex_lock(&g_adopt_mu);
+    for (size_t i = 0; i < g_adopt_len;) {
+        if (g_adopt[i].owner == owner) {
+            Tensor* in = g_adopt[i].internal;
+            g_adopt[i] = g_adopt[--g_adopt_len];
+            pthread_mutex_unlock(&g_adopt_mu);
+            if (in->device == DEVICE_GPU && in->gpu_buffer) reg_release(in->gpu_buffer);
+            in->device = DEVICE_CPU;
+            in->gpu_buffer = 0;
+            pthread_mutex_lock(&g_adopt_mu);
+        } else {
+            i++;
+        }
+    }
+    pthread_mutex_unlock(&g_adopt_mu);
+}
+
 /* src/rpl_core.c:72-77, plus the device buffers */
 void tensor_free(Tensor* t) {
     if (!t) return;
     if (t->device == DEVICE_GPU && t->gpu_buffer) reg_release(t->gpu_buffer);
+    release_adopted(t);
     free(t->_allocation);
     free(t->grad);
     free(t);

@@ -37,6 +37,23 @@ def test_sgemm_nan_in_c_propagates(gpu, golden):
     np.testing.assert_allclose(out[~np.isnan(ref)], ref[~np.isnan(ref)], rtol=1e-6)
 
 
+def test_sgemm_split_k_nan_in_c(gpu):
+    # tensor_gemm reads C even when beta == 0 (src/rpl_core.c:214): a NaN in C
+    # survives the split-K reduction too.
+    rng = np.random.default_rng(3)
+    M, N, K = 8, 8, 1024
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    C0 = np.zeros((M, N), np.float32)
+    C0[2, 3] = np.nan
+    say("sgemm split-K nan")
+    out = sgemm(A, B, C0, M, N, K, 1.0, 0.0)
+    assert np.isnan(out[2, 3]) and np.isnan(out).sum() == 1
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    mask = ~np.isnan(out)
+    assert np.max(np.abs(out[mask] - ref[mask]) / (np.abs(A) @ np.abs(B))[mask]) <= fp32_tol(K)
+
+
 def test_sgemm_known_answers(gpu):
     # tests/full_system_check.py:33-37 and examples/gpu_test.c:106-128 (exact)
     say("sgemm known answers")
@@ -49,8 +66,11 @@ def test_sgemm_known_answers(gpu):
     assert np.array_equal(sgemm(A, np.eye(256, dtype=np.float32), np.zeros_like(A), 256, 256, 256), A)
 
 
+# (17, 33, 2049), (128, 784, 4096), (10, 128, 4096) and (512, 512, 512) take
+# the split-K path (few 128 x 128 tiles, long K): partial tiles in a
+# workspace, then C = alpha * sum + beta * C.
 SHAPES = [(1, 1, 1), (3, 5, 7), (127, 129, 65), (130, 7, 300), (64, 256, 32), (200, 130, 1), (17, 33, 2049),
-          (256, 256, 0)]
+          (256, 256, 0), (128, 784, 4096), (10, 128, 4096), (512, 512, 512)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
