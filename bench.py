@@ -344,11 +344,14 @@ def main():
                "sample": f"oracle gemm_int8 (reference ops_extended.c:83-123 restated, -O3 -fopenmp) on a "
                          f"{args.cpu_rows}x{n}x{n} row slab of the same quantized inputs, {cpu_s:.1f} s"}
 
-    traffic = None
+    # HBM/MALL bytes per launch of the roofline kernel, from the committed
+    # FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel of known size).
+    traffic, traffic_kernel = None, "k_gemm_i8_nt_dma<0>"
     tpath = os.path.join(REPO, "profiles", "traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("gemm_i8_nt_8192", {}).get("bytes_per_launch")
+            rec = json.load(f).get("gemm_i8_nt_8192", {})
+        traffic, traffic_kernel = rec.get("bytes_per_launch"), rec.get("kernel", traffic_kernel)
 
     out = {
         "metric": METRIC,
@@ -371,7 +374,7 @@ def main():
                  "pct_peak": round(100 * tflops / PEAK_FP32_TFLOPS, 2), "dtype": "f32"},
         "roofline": {"bound": "mfma", "achieved": round(kern_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": round(kern_tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
-                     "kernel": "k_gemm_i8_nt (int8 ops/s)", "ms_per_launch": round(ms_k, 4)},
+                     "kernel": traffic_kernel, "ms_per_launch": round(ms_k, 4)},
         "roofline_fp32": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4), "kernel": "k_sgemm"},
         "skinny_int8": skinny,

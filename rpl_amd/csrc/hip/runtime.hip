@@ -75,19 +75,129 @@ int check_launch(const char* what) {
     return RPLHIP_OK;
 }
 
+// ---------------------------------------------------------------- workspaces
+//
+// Temporary device memory of one call (split-K partials, reduction partials,
+// the transposed B of gemm_int8).  hipMallocAsync/hipFreeAsync cost 10-25 us
+// each on the host, which dominated small training steps, so blocks are
+// cached instead.  A block released on stream S is handed out again only to
+// a later request on S: stream order then runs the new user's kernels after
+// the old user's.  Blocks are given back to HIP only after a device-wide
+// synchronisation (trim), so no kernel can still be using them.
+struct WsBlock {
+    void* p;
+    size_t bytes;        // size class (see ws_class)
+    hipStream_t stream;  // stream of the last user
+    bool idle;           // true: no queued work uses it; any stream may take it
+    bool in_use;
+};
+static pthread_mutex_t g_ws_mu = PTHREAD_MUTEX_INITIALIZER;
+static WsBlock* g_ws;
+static size_t g_ws_len, g_ws_cap, g_ws_cached;
+// Cached bytes above which unused blocks are returned before a new one is made.
+constexpr size_t kWsRetainBytes = size_t(4) << 30;
+
+// Four size classes per power of two (<= 25% slack), at least 256 B.
+static size_t ws_class(size_t b) {
+    if (b <= 256) return 256;
+    int lg = 63 - __builtin_clzll((unsigned long long)(b - 1));
+    size_t step = size_t(1) << (lg - 2);
+    return (b + step - 1) / step * step;
+}
+
+// Free every unused block; the caller holds g_ws_mu.  Synchronises the device.
+static void ws_trim_locked() {
+    bool any = false;
+    for (size_t i = 0; i < g_ws_len; i++) any |= !g_ws[i].in_use;
+    if (!any) return;
+    if (hipDeviceSynchronize() != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
+    size_t j = 0;
+    for (size_t i = 0; i < g_ws_len; i++) {
+        if (g_ws[i].in_use) {
+            g_ws[j++] = g_ws[i];
+        } else {
+            (void)hipFree(g_ws[i].p);
+            g_ws_cached -= g_ws[i].bytes;
+        }
+    }
+    g_ws_len = j;
+}
+
+static void ws_trim() {
+    pthread_mutex_lock(&g_ws_mu);
+    ws_trim_locked();
+    pthread_mutex_unlock(&g_ws_mu);
+}
+
 int ws_alloc(void** p, size_t bytes, hipStream_t stream) {
     *p = nullptr;
     if (bytes == 0) return RPLHIP_OK;
-    hipError_t e = hipMallocAsync(p, bytes, stream);
+    const size_t cls = ws_class(bytes);
+    pthread_mutex_lock(&g_ws_mu);
+    for (size_t i = 0; i < g_ws_len; i++) {
+        WsBlock& b = g_ws[i];
+        if (!b.in_use && b.bytes == cls && (b.idle || b.stream == stream)) {
+            b.in_use = true;
+            b.idle = false;
+            b.stream = stream;
+            *p = b.p;
+            pthread_mutex_unlock(&g_ws_mu);
+            return RPLHIP_OK;
+        }
+    }
+    if (g_ws_cached + cls > kWsRetainBytes) ws_trim_locked();
+    if (g_ws_len == g_ws_cap) {
+        size_t nc = g_ws_cap ? 2 * g_ws_cap : 32;
+        WsBlock* nb = (WsBlock*)realloc(g_ws, nc * sizeof(WsBlock));
+        if (!nb) {
+            pthread_mutex_unlock(&g_ws_mu);
+            return fail(RPLHIP_ERR_NOMEM, "workspace table of %zu entries", nc);
+        }
+        g_ws = nb;
+        g_ws_cap = nc;
+    }
+    void* q = nullptr;
+    hipError_t e = hipMalloc(&q, cls);
+    if (e == hipErrorOutOfMemory) {
+        (void)hipGetLastError();
+        ws_trim_locked();
+        e = hipMalloc(&q, cls);
+    }
     if (e != hipSuccess) {
-        *p = nullptr;
+        (void)hipGetLastError();
+        pthread_mutex_unlock(&g_ws_mu);
         return fail(RPLHIP_ERR_NOMEM, "workspace of %zu bytes: %s", bytes, hipGetErrorString(e));
     }
+    g_ws[g_ws_len++] = WsBlock{q, cls, stream, false, true};
+    g_ws_cached += cls;
+    *p = q;
+    pthread_mutex_unlock(&g_ws_mu);
     return RPLHIP_OK;
 }
 
 void ws_free(void* p, hipStream_t stream) {
-    if (p) (void)hipFreeAsync(p, stream);
+    if (!p) return;
+    pthread_mutex_lock(&g_ws_mu);
+    for (size_t i = 0; i < g_ws_len; i++) {
+        if (g_ws[i].p == p) {
+            g_ws[i].in_use = false;
+            g_ws[i].stream = stream;
+            break;
+        }
+    }
+    pthread_mutex_unlock(&g_ws_mu);
+}
+
+// `s` has no queued work left (all = every stream): its unused blocks may go
+// to any stream.
+static void ws_stream_idle(hipStream_t s, bool all = false) {
+    pthread_mutex_lock(&g_ws_mu);
+    for (size_t i = 0; i < g_ws_len; i++)
+        if (!g_ws[i].in_use && (all || g_ws[i].stream == s)) g_ws[i].idle = true;
+    pthread_mutex_unlock(&g_ws_mu);
 }
 
 int cu_count() { return g_cu_count > 0 ? g_cu_count : 256; }
@@ -116,6 +226,12 @@ int rplhip_malloc(void** ptr, size_t bytes) {
     RPLHIP_REQUIRE_DEVICE();
     if (bytes == 0) return RPLHIP_OK;
     hipError_t e = hipMalloc(ptr, bytes);
+    if (e == hipErrorOutOfMemory) {
+        // Give the cached workspaces back first.
+        (void)hipGetLastError();
+        ws_trim();
+        e = hipMalloc(ptr, bytes);
+    }
     if (e != hipSuccess) {
         *ptr = nullptr;
         return fail(RPLHIP_ERR_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
@@ -165,6 +281,7 @@ int rplhip_memset(void* ptr, int value, size_t bytes, rplhip_stream_t s) {
 int rplhip_synchronize(void) {
     RPLHIP_REQUIRE_DEVICE();
     RPLHIP_CHECK(hipDeviceSynchronize());
+    ws_stream_idle(nullptr, true);
     return RPLHIP_OK;
 }
 
@@ -180,6 +297,10 @@ int rplhip_stream_create(rplhip_stream_t* s) {
 int rplhip_stream_destroy(rplhip_stream_t s) {
     if (!s) return RPLHIP_OK;
     RPLHIP_REQUIRE_DEVICE();
+    // Drain it first so the workspaces it used are free for other streams
+    // (a later stream may be given the same handle).
+    RPLHIP_CHECK(hipStreamSynchronize(as_stream(s)));
+    ws_stream_idle(as_stream(s));
     RPLHIP_CHECK(hipStreamDestroy(as_stream(s)));
     return RPLHIP_OK;
 }
@@ -187,6 +308,7 @@ int rplhip_stream_destroy(rplhip_stream_t s) {
 int rplhip_stream_synchronize(rplhip_stream_t s) {
     RPLHIP_REQUIRE_DEVICE();
     RPLHIP_CHECK(hipStreamSynchronize(as_stream(s)));
+    ws_stream_idle(as_stream(s));
     return RPLHIP_OK;
 }
 

@@ -201,3 +201,41 @@ def test_parallel_gemm_optimized(gpu, orc, golden):
     lib.parallel_gemm_optimized(A.ctypes.data_as(fp), B.ctypes.data_as(fp), out.ctypes.data_as(fp), M, N, K)
     ref = orc.sgemm(A, B, C1, M, N, K, 1.0, 1.0)
     assert gemm_err_ratio(out, A, B, ref, 1.0, 1.0, C1) <= fp32_tol(K)
+
+
+def test_workspace_reuse_across_streams(gpu):
+    # Split-K GEMMs keep their partial tiles in cached workspace blocks; a
+    # block is reused only in the stream order of its last user.  Queue
+    # calls of two shapes on two streams without synchronising in between,
+    # destroy one stream half way, and check every result.
+    lib = rpl_amd.lib()
+    from rpl_amd import DeviceBuffer, check
+    rng = np.random.default_rng(11)
+    streams = []
+    for _ in range(3):
+        s = C.c_void_p()
+        check(lib.rplhip_stream_create(C.byref(s)), "stream_create")
+        streams.append(s)
+    jobs = []
+    for i in range(12):
+        M, N, K = ((10, 128, 4096), (128, 784, 4096), (17, 33, 2049))[i % 3]
+        A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+        B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+        dA, dB, dC = DeviceBuffer.from_array(A), DeviceBuffer.from_array(B), DeviceBuffer.from_array(
+            np.zeros((M, N), np.float32))
+        s = streams[2] if i >= 6 and i % 2 == 0 else streams[i % 2]
+        check(lib.rplhip_sgemm(0, 0, M, N, K, 1.0, dA.ptr, K, dB.ptr, N, 0.0, dC.ptr, N, s), "sgemm")
+        jobs.append((A, B, dA, dB, dC, M, N, K))
+        if i == 5:
+            check(lib.rplhip_stream_destroy(streams[0]), "stream_destroy")
+            streams[0] = C.c_void_p()
+            check(lib.rplhip_stream_create(C.byref(streams[0])), "stream_create")
+    say("workspace reuse across streams", len(jobs))
+    for s in streams:
+        check(lib.rplhip_stream_synchronize(s), "stream_synchronize")
+    for A, B, dA, dB, dC, M, N, K in jobs:
+        out = dC.to_array(np.float32, (M, N))
+        ref = A.astype(np.float64) @ B.astype(np.float64)
+        assert np.max(np.abs(out - ref) / (np.abs(A) @ np.abs(B))) <= fp32_tol(K)
+    for s in streams:
+        check(lib.rplhip_stream_destroy(s), "stream_destroy")
