@@ -74,6 +74,19 @@ __device__ __forceinline__ int32_t x86_cvt_i32(float f) {
     return (int32_t)f;
 }
 
+// x86_cvt_i32(roundf(y)) for every float y, in four VALU operations:
+// roundf(y) == trunc(y + copysign(0.49999997f, y)) when the sum is rounded
+// to nearest-even (0.49999997f is the float just below 0.5), and the range
+// test on the sum is the range test on the rounded value.  Checked against
+// glibc roundf + cvttss2si for all 2^32 floats (tests/test_round_identity.py).
+// The add must stay a separately rounded operation, never an FMA with the
+// product that feeds it, hence contract(off) here and in its callers.
+__device__ __forceinline__ int32_t x86_round_cvt(float y) {
+#pragma clang fp contract(off)
+    const float t = y + __builtin_copysignf(0.49999997f, y);
+    return (t >= -2147483648.0f && t < 2147483648.0f) ? (int32_t)t : INT32_MIN;
+}
+
 // Wrapping int32 add (the reference's signed adds wrap on x86).
 __device__ __forceinline__ int32_t wrap_add(int32_t a, int32_t b) {
     return (int32_t)((uint32_t)a + (uint32_t)b);

@@ -1,41 +1,34 @@
 // INT8 GEMMs on gfx950, int32 accumulation.
 //
-// Core kernel: NT layout (A [M,K] and B [N,K], both k-contiguous), which is
-// what the MFMA operands want: every lane feeds 16 consecutive k bytes of one
-// row.  v_mfma_i32_32x32x32_i8 (65536 ops per 32-cycle issue; it sustains
-// close to peak from one wave per SIMD, where 16x16x64 with the same
-// accumulator count does not).  Block tile BM x BN x 64 staged through LDS in
-// 4 stages of 64-byte rows whose four 16-byte chunks are XOR-swizzled, so both
-// the 128-bit fragment reads and the 128-bit tile writes are conflict-free;
-// 4 waves (2 x 2), each owning a (BM/2) x (BN/2) sub-tile of 32x32 MFMA
-// blocks.  The large configuration (256 x 256, 128 x 128 per wave, the 256
-// int32 accumulators living in AGPRs) halves the LDS bytes read per MFMA op
-// compared with 64 x 64 wave tiles.  Pipeline: HBM loads two tiles ahead (two
-// register sets), LDS one tile ahead, fragments double-buffered per 32-k step,
-// one barrier per tile.  Global loads are 128-bit raw buffer loads whose
-// resource ends at the last existing row, so M and N edges zero-fill in
-// hardware.  Tiles are visited in an XCD-aware grouped order: workgroups are
-// dispatched round-robin over the 8 XCDs, so consecutive tile indices are
-// remapped onto one XCD and grouped 8 tile-rows at a time, which keeps the A
-// and B panels the XCD's 32 CUs share resident in that XCD's L2.
+// All kernels take the NT layout (A [M,K] and B [N,K], both k-contiguous),
+// which is what the i8 MFMA operands want: every lane feeds 16 consecutive
+// k-bytes of one row.  gemm_int8's B is [K,N] (n-contiguous); it is first
+// transposed into a workspace so the NT kernels serve both layouts.
+//
+// Which kernel runs (run_nt):
+//   M <= 16, K % 64 == 0, K <= 16384, aligned : k_skinny, an HBM-streaming
+//       kernel (whole rows of B per load instruction, VGPR landing, LDS
+//       permute into v_mfma_i32_16x16x64_i8 fragments, waves split K).
+//   M <= 4 otherwise                          : k_gemv_i8_dot4 (VALU dot4).
+//   4 < M <= 16 otherwise                     : k_gemv_i8_nt (MFMA, byte-safe).
+//   >= 2 tiles of 256 x 256 per CU, aligned, K % 64 == 0, operands < 2 GiB :
+//       k_gemm_i8_nt_dma, 256 x 256 x 64 tiles, one wave per SIMD with a
+//       128 x 128 wave tile of v_mfma_i32_32x32x32_i8 (accumulators in
+//       AGPRs), HBM -> LDS copies done by the load unit (buffer_load ... lds)
+//       into a 4-stage ring, epilogue stored straight from the accumulators.
+//   everything else                           : k_gemm_i8_nt<Cfg<128,128>>
+//       (or <256,256> for big unaligned-K shapes), register-staged pipeline,
+//       byte-safe loads for odd K / alignment.
+// Tiles are visited in an XCD-aware grouped order (rplhip::tile_of): the 8
+// XCDs each take a contiguous range of tiles, walked 8 tile-rows at a time,
+// so the A and B panels an XCD's 32 CUs share stay in that XCD's L2.
 //
 // The epilogue is fused and selected at compile time:
-//   kRaw     : out = acc + bias[n]                      (linear_int8)
-//   kRequant : out = x86((int32)roundf(((float)acc*sa)*sb/sc)), optional
-//              zero-point correction                     (gemm_int8)
-//   kDequant : y = ((float)acc * sx[m|0]) * sw[n|0]      (fused fp32 output)
-// It is staged through LDS so every lane writes four consecutive outputs.
-//
-// gemm_int8's B is [K,N] (n-contiguous); it is first transposed into a
-// stream-ordered workspace so the NT core serves both layouts.
-//
-// Decode shapes: M <= 4 runs a VALU kernel (v_dot4_i32_i8) in which each wave
-// streams whole rows of B, 1 KB per load instruction, with A staged once per
-// block in LDS.  4 < M <= 16 runs an MFMA bandwidth kernel: 16 waves per block
-// split K, each lane streams 16-byte chunks of B straight from HBM into MFMA
-// operands (A, padded to 16 rows, is the other operand and is reused across
-// the block's two 16-row B panels), and the 16 partial tiles are reduced
-// through LDS before the epilogue.
+//   kRaw         : out = acc + bias[n]                       (linear_int8)
+//   kRequant     : out = x86((int32)roundf(((float)acc*sa)*sb/sc)), optional
+//                  zero-point correction                      (gemm_int8)
+//   kRequantPow2 : kRequant with sc = +-2^k, where x/sc == x*(1/sc) exactly
+//   kDequant     : y = ((float)acc * sx[m|0]) * sw[n|0]       (fused fp32 output)
 #include <math.h>
 #include <stdlib.h>
 
@@ -79,27 +72,40 @@ struct EpiParams {
     uint32_t ldc;
 };
 
+// Output bits of element (m, n) from its accumulator.  cadd / cmul / rmul
+// are the per-column bias, per-column and per-row dequant scales when the
+// caller has them at hand (kRaw / kDequant); the float operation order is
+// the reference's (src/ops_extended.c:119).
 template <int EPI>
-__device__ __forceinline__ void epilogue_store(const EpiParams& p, uint32_t m, uint32_t n, int32_t acc) {
-    uint64_t o = (uint64_t)m * p.ldc + n;
-    if (EPI == kRaw) {
-        int32_t v = acc;
-        if (p.bias) v = wrap_add(v, (int32_t)p.bias[n]);
-        p.out_i32[o] = v;
-    } else if (EPI == kRequant) {
+__device__ __forceinline__ uint32_t epi_bits(const EpiParams& p, int32_t acc, uint32_t m, uint32_t n, int32_t cadd,
+                                             float rmul, float cmul) {
+#pragma clang fp contract(off)
+    if constexpr (EPI == kRaw) {
+        return (uint32_t)wrap_add(acc, cadd);
+    } else if constexpr (EPI == kRequant) {
         int32_t v = acc;
         if (p.rowsum_a) v = wrap_add(v, -wrap_mul(p.zb, p.rowsum_a[m]));
         if (p.rowsum_b) v = wrap_add(v, -wrap_mul(p.za, p.rowsum_b[n]));
         v = wrap_add(v, p.kzz);
-        float result = (float)v * p.sa * p.sb / p.sc;  // ops_extended.c:119
-        p.out_i32[o] = x86_cvt_i32(roundf(result));
-    } else if (EPI == kRequantPow2) {
-        float result = (float)acc * p.sa * p.sb * p.inv_sc;
-        p.out_i32[o] = x86_cvt_i32(roundf(result));
+        return (uint32_t)x86_round_cvt((float)v * p.sa * p.sb / p.sc);
+    } else if constexpr (EPI == kRequantPow2) {
+        return (uint32_t)x86_round_cvt((float)acc * p.sa * p.sb * p.inv_sc);
     } else {
-        float v = (float)acc * p.sx[p.sx_per_row ? m : 0];
-        p.out_f32[o] = v * p.sw[p.sw_per_col ? n : 0];
+        return __float_as_uint((float)acc * rmul * cmul);
     }
+}
+
+template <int EPI>
+__device__ __forceinline__ void epilogue_store(const EpiParams& p, uint32_t m, uint32_t n, int32_t acc) {
+    const uint64_t o = (uint64_t)m * p.ldc + n;
+    const int32_t cadd = (EPI == kRaw && p.bias) ? (int32_t)p.bias[n] : 0;
+    const float rmul = EPI == kDequant ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
+    const float cmul = EPI == kDequant ? p.sw[p.sw_per_col ? n : 0] : 0.0f;
+    const uint32_t bits = epi_bits<EPI>(p, acc, m, n, cadd, rmul, cmul);
+    if constexpr (EPI == kDequant)
+        p.out_f32[o] = __uint_as_float(bits);
+    else
+        p.out_i32[o] = (int32_t)bits;
 }
 
 // Load one 16-byte chunk (row r, byte column k) of a k-contiguous matrix with
@@ -209,41 +215,17 @@ struct Frags {
 template <int EPI>
 __device__ __forceinline__ void epilogue_store4(const EpiParams& p, uint32_t m, uint32_t n, uint32_t N, v4i v) {
     const uint64_t o = (uint64_t)m * p.ldc + n;
-    const bool vec = n + 3 < N && (p.ldc & 3) == 0;
-    if (EPI == kDequant) {
-        const float s = p.sx[p.sx_per_row ? m : 0];
-        float4 y;
-        y.x = (float)v[0] * s * p.sw[p.sw_per_col ? n + 0 : 0];
-        y.y = (float)v[1] * s * p.sw[p.sw_per_col ? n + 1 : 0];
-        y.z = (float)v[2] * s * p.sw[p.sw_per_col ? n + 2 : 0];
-        y.w = (float)v[3] * s * p.sw[p.sw_per_col ? n + 3 : 0];
-        if (vec && (((uintptr_t)p.out_f32) & 15) == 0) {
-            *reinterpret_cast<float4*>(p.out_f32 + o) = y;
-        } else {
-            if (n + 0 < N) p.out_f32[o + 0] = y.x;
-            if (n + 1 < N) p.out_f32[o + 1] = y.y;
-            if (n + 2 < N) p.out_f32[o + 2] = y.z;
-            if (n + 3 < N) p.out_f32[o + 3] = y.w;
-        }
-    } else if (vec && (((uintptr_t)p.out_i32) & 15) == 0) {
+    void* out = EPI == kDequant ? (void*)(p.out_f32 + o) : (void*)(p.out_i32 + o);
+    if (n + 3 < N && (p.ldc & 3) == 0 && (((uintptr_t)out) & 15) == 0) {
+        const float rmul = EPI == kDequant ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
         v4i r;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            int32_t x = v[e];
-            if (EPI == kRaw) {
-                if (p.bias) x = wrap_add(x, (int32_t)p.bias[n + e]);
-            } else if (EPI == kRequantPow2) {
-                x = x86_cvt_i32(roundf((float)x * p.sa * p.sb * p.inv_sc));
-            } else {
-                if (p.rowsum_a) x = wrap_add(x, -wrap_mul(p.zb, p.rowsum_a[m]));
-                if (p.rowsum_b) x = wrap_add(x, -wrap_mul(p.za, p.rowsum_b[n + e]));
-                x = wrap_add(x, p.kzz);
-                float result = (float)x * p.sa * p.sb / p.sc;  // ops_extended.c:119
-                x = x86_cvt_i32(roundf(result));
-            }
-            r[e] = x;
+            const int32_t cadd = (EPI == kRaw && p.bias) ? (int32_t)p.bias[n + e] : 0;
+            const float cmul = EPI == kDequant ? p.sw[p.sw_per_col ? n + e : 0] : 0.0f;
+            r[e] = (int32_t)epi_bits<EPI>(p, v[e], m, n + e, cadd, rmul, cmul);
         }
-        *reinterpret_cast<v4i*>(p.out_i32 + o) = r;
+        *reinterpret_cast<v4i*>(out) = r;
     } else {
 #pragma unroll
         for (int e = 0; e < 4; e++)
@@ -441,12 +423,12 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt(const int8_t* __restrict_
 // r%4 and column nb + j*32, where mb = tile row + 4*(l/32) and nb = tile
 // column + l%32.  Fully unrolled (the accumulators are only ever indexed by
 // constants); values that depend on the column are loaded once per block
-// column, those that depend on the row once per row; interior tiles (`full`)
-// skip the bounds checks.  Each store instruction writes two 128-byte row
-// segments.
+// column, those that depend on the row once per row.  Each store
+// instruction writes two 128-byte row segments.  This is the bounds-checked
+// form for edge tiles; epilogue_tile_full serves interior ones.
 template <int EPI, int FM, int FN>
 __device__ __forceinline__ void epilogue_tile(const EpiParams& p, const v16i (&acc)[FM][FN], uint32_t mb,
-                                              uint32_t nb, uint32_t M, uint32_t N, bool full) {
+                                              uint32_t nb, uint32_t M, uint32_t N) {
     int32_t cadd[FN];  // kRaw: bias[n]
     float cmul[FN];    // kDequant: sw[n]
 #pragma unroll
@@ -460,24 +442,63 @@ __device__ __forceinline__ void epilogue_tile(const EpiParams& p, const v16i (&a
         static_for<16>([&](auto R) {
             constexpr int r = decltype(R)::value;
             const uint32_t m = mb + i * 32 + 8 * (r / 4) + r % 4;
-            const bool row_ok = full || m < M;
-            const float rmul = (EPI == kDequant && row_ok) ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
+            if (m >= M) return;
+            const float rmul = EPI == kDequant ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
             static_for<FN>([&](auto J) {
                 constexpr int j = decltype(J)::value;
                 const uint32_t n = nb + j * 32;
-                if (full || (row_ok && n < N)) {
+                if (n < N) {
+                    const uint32_t bits = epi_bits<EPI>(p, acc[i][j][r], m, n, cadd[j], rmul, cmul[j]);
                     const uint64_t o = (uint64_t)m * p.ldc + n;
-                    const int32_t a = acc[i][j][r];
-                    if constexpr (EPI == kRaw) {
-                        p.out_i32[o] = wrap_add(a, cadd[j]);
-                    } else if constexpr (EPI == kRequantPow2) {
-                        p.out_i32[o] = x86_cvt_i32(roundf((float)a * p.sa * p.sb * p.inv_sc));
-                    } else if constexpr (EPI == kDequant) {
-                        p.out_f32[o] = (float)a * rmul * cmul[j];
-                    } else {
-                        epilogue_store<EPI>(p, m, n, a);
-                    }
+                    if constexpr (EPI == kDequant)
+                        p.out_f32[o] = __uint_as_float(bits);
+                    else
+                        p.out_i32[o] = (int32_t)bits;
                 }
+            });
+        });
+    });
+}
+
+// Largest ldc for which a 128-row wave sub-tile spans < 2^31 bytes of C.
+constexpr uint32_t kFullEpiMaxLdc = 1u << 21;
+
+// The same for a wave sub-tile of FM*32 x FN*32 outputs that lies wholly
+// inside C (origin wm0, wn0, wave-uniform), with FM*32*ldc*4 < 2^31.  The
+// stores are raw buffer stores whose address needs no VALU work: the
+// resource is based at the sub-tile origin, the lane's part (row 4*(l/32),
+// column l%32) is one VGPR offset, the row of result register r (a
+// constant times ldc) goes in the scalar offset and the 32-column block in
+// the instruction's immediate offset.
+template <int EPI, int FM, int FN>
+__device__ __forceinline__ void epilogue_tile_full(const EpiParams& p, const v16i (&acc)[FM][FN], uint32_t wm0,
+                                                   uint32_t wn0, uint32_t lane) {
+    const uint32_t ldc4 = p.ldc * 4;
+    const void* out = EPI == kDequant ? (const void*)p.out_f32 : (const void*)p.out_i32;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        uniform_rsrc((const char*)out + ((uint64_t)wm0 * p.ldc + wn0) * 4, FM * 32 * ldc4);
+    const uint32_t voff = 4 * (lane / 32) * ldc4 + (lane % 32) * 4;
+    const uint32_t mb = wm0 + 4 * (lane / 32), nb = wn0 + lane % 32;
+    int32_t cadd[FN];
+    float cmul[FN];
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const uint32_t n = nb + j * 32;
+        cadd[j] = (EPI == kRaw && p.bias) ? (int32_t)p.bias[n] : 0;
+        cmul[j] = EPI == kDequant ? p.sw[p.sw_per_col ? n : 0] : 0.0f;
+    }
+    static_for<FM>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        static_for<16>([&](auto R) {
+            constexpr int r = decltype(R)::value;
+            constexpr uint32_t row = i * 32 + 8 * (r / 4) + r % 4;
+            const uint32_t m = mb + row;
+            const float rmul = EPI == kDequant ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
+            const int soff = (int)__builtin_amdgcn_readfirstlane(row * ldc4);
+            static_for<FN>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                const uint32_t bits = epi_bits<EPI>(p, acc[i][j][r], m, nb + j * 32, cadd[j], rmul, cmul[j]);
+                __builtin_amdgcn_raw_buffer_store_b32(bits, rsrc, (int)(voff + j * 128), soff, 0);
             });
         });
     });
@@ -697,8 +718,10 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
         mma(f1);
     }
 
-    epilogue_tile<EPI, 4, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * 128 + lane % 32, M, N,
-                             m0 + BM <= M && n0 + BN <= N);
+    if (m0 + BM <= M && n0 + BN <= N && p.ldc <= kFullEpiMaxLdc)
+        epilogue_tile_full<EPI, 4, 4>(p, acc, m0 + wm * 128, n0 + wn * 128, lane);
+    else
+        epilogue_tile<EPI, 4, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * 128 + lane % 32, M, N);
 }
 
 // --------------------------- NT core GEMM, 8-wave ping-pong (2 waves/SIMD)
@@ -840,8 +863,10 @@ __global__ void __launch_bounds__(512, 1) k_gemm_i8_nt_pp(const int8_t* __restri
     }
     if (grp == 0) __builtin_amdgcn_s_barrier();  // group 0 ends one phase earlier
 
-    epilogue_tile<EPI, 4, 2>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * 64 + lane % 32, M, N,
-                             m0 + BM <= M && n0 + BN <= N);
+    if (m0 + BM <= M && n0 + BN <= N && p.ldc <= kFullEpiMaxLdc)
+        epilogue_tile_full<EPI, 4, 2>(p, acc, m0 + wm * 128, n0 + wn * 64, lane);
+    else
+        epilogue_tile<EPI, 4, 2>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * 64 + lane % 32, M, N);
 }
 
 // --------------------------------------------------- skinny (M <= 16) GEMM

@@ -220,9 +220,9 @@ def _requant_f32(acc, sa, sb, sc):
 
 # Shapes with >= 2 tiles of 256 x 256 per CU take the direct-to-LDS kernel
 # (k_gemm_i8_nt_dma); K = 448 and 832 run its steady-state loop and tails of
-# 3 and 5 tiles.  gemm_int8 reads B [K,N] in place (transposed LDS reads)
-# when N % 16 == 0 (5888, 6144) and transposes it first otherwise (5900);
-# the first two shapes have ragged edges in M and N.
+# 3 and 5 tiles.  The first two shapes have ragged edges in M and N, so both
+# the bounds-checked epilogue (edge tiles) and the unchecked buffer-store
+# epilogue (interior tiles) run; gemm_int8 transposes B [K,N] first.
 BIG = [(5890, 5900, 832), (5890, 5888, 832), (6144, 6144, 448)]
 
 
@@ -244,8 +244,11 @@ def test_big_tile_int8_paths(gpu, orc, M, N, K):
     a64 = acc.astype(np.int64)
     assert np.array_equal(a64.sum(1), A.astype(np.int64) @ Bt.astype(np.int64).sum(0))
     assert np.array_equal(a64.sum(0), Bt.astype(np.int64) @ A.astype(np.int64).sum(0))
-    # gemm_int8 requant: power-of-two sc (exact-reciprocal epilogue) and a generic sc.
-    for sa, sb, sc in ((0.013, 0.7, 0.25), (1.5, -3.0, -4.0), (2.0 ** 20, 2.0 ** 20, 2.0 ** -100), (0.013, 0.7, 0.3)):
+    # gemm_int8 requant: power-of-two sc (exact-reciprocal epilogue) and a
+    # generic sc; exact .5 ties (acc / 2, acc / 2 via 1/sc), overflow, and
+    # sc = 0 / sa = inf (inf and NaN quantize to INT32_MIN).
+    for sa, sb, sc in ((0.013, 0.7, 0.25), (1.5, -3.0, -4.0), (2.0 ** 20, 2.0 ** 20, 2.0 ** -100), (0.013, 0.7, 0.3),
+                       (0.5, 1.0, 1.0), (1.0, 1.0, 2.0), (1.0, 1.0, 3.0), (0.013, 0.7, 0.0), (np.inf, 1.0, 1.0)):
         out = empty((M, N), np.int32)
         say("big-tile gemm_int8", M, N, K, sa, sb, sc)
         rpl_amd.check(lib.rplhip_gemm_int8(dA.ptr, dB.ptr, out.ptr, M, N, K, sa, sb, sc, 0, 0, None))

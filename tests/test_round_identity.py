@@ -1,0 +1,23 @@
+"""The requantizing GEMM epilogues round with
+x86_round_cvt(y) = trunc(y + copysign(0.49999997f, y)) plus one range test
+(rpl_amd/csrc/hip/common.h) instead of roundf + cvttss2si.  This checks the
+identity for all 2^32 float bit patterns on the CPU, against glibc roundf
+(the function the reference calls, src/ops_extended.c:119-120)."""
+import os
+import shutil
+import subprocess
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_round_identity_all_floats(tmp_path):
+    exe = tmp_path / "round_identity"
+    subprocess.run(["gcc", "-O2", "-fopenmp", "-ffp-contract=off", "-fno-fast-math", "-o", str(exe),
+                    os.path.join(HERE, "round_identity.c"), "-lm"], check=True)
+    env = dict(os.environ, OMP_NUM_THREADS=str(min(8, os.cpu_count() or 1)))
+    r = subprocess.run([str(exe)], capture_output=True, text=True, env=env, timeout=600)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.strip() == "mismatches 0"
