@@ -14,9 +14,17 @@
 // Both give lane l the k index 4*(l/16) + s of substep s, so A and B agree.
 // With B stored [K,N] the interleaved output columns make every lane own 4
 // consecutive columns, so C is read and written with 128-bit accesses.
-#include "common.h"
+#include <stdlib.h>
+
+#include "mfma_pipe.h"
 
 namespace {
+
+using rplhip::lds_ptr;
+using rplhip::static_for;
+using rplhip::swz;
+using rplhip::uniform_rsrc;
+using rplhip::waitcnt_imm;
 
 constexpr int BM = 128, BN = 128, BK = 32;
 constexpr int kThreads = 256;
@@ -237,6 +245,262 @@ __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, u
     }
 }
 
+// ------------------------------------------ direct-to-LDS kernel (big grids)
+//
+// For grids with several 256 x 256 tiles per CU (8192^3: four).  Block tile
+// 256 x 256 x 16, 4 waves (2 x 2) of 128 x 128, one wave per SIMD, on
+// v_mfma_f32_32x32x2f32 (4096 flops per 64-cycle issue) with the 16 x 16
+// accumulator registers per 32 x 32 block in AGPRs.  The load unit copies
+// the tiles HBM -> LDS itself (buffer_load_dword x4 ... lds, 1 KB per
+// instruction) into a ring of S stages; one barrier per 16-k tile, between
+// its two 8-k halves.  A 16-k tile is 64 flops per byte of LDS traffic, so
+// each stage carries 8192 MFMA cycles per wave: latency hides easily.
+//
+// Operand kinds, both 16 KB per stage:
+//  * k-contiguous (A as [M,K], B as [N,K]): 256 rows of 64 bytes, the four
+//    16-byte k-chunks of row r at slot c ^ swz(r); one copy instruction moves
+//    16 rows (lane l: row l/4, chunk (l%4) ^ swz(row) chosen at the source).
+//    Fragment read for half t: lane l reads chunk l/32 + 2t of row l%32 of
+//    each 32-row block -> floats k = 4(l/32) + 8t + s, s = 0..3: one 128-bit
+//    read serves the block's four substeps.
+//  * row-contiguous (A as [K,M], B as [K,N]): 16 k-rows of 1 KB; one copy
+//    instruction moves one k-row.  The wave's four blocks interleave their
+//    rows (block f owns tile rows wofs + 4c + f), so lane l reading floats
+//    wofs + 4(l%32) .. +3 of k-row 4(l/32) + 8t + s gets substep s of all
+//    four blocks in one 128-bit read.
+// Both kinds give lane l the same k for (t, s), so A and B agree.  Rows past
+// the matrix are clamped to the last row and columns to the last 4 (their
+// products are never stored), so no copy leaves the operand.
+// Requires K % 16 == 0, 16-byte aligned bases, ld % 4 == 0, N % 4 == 0
+// (and M % 4 == 0 for A as [K,M]), operands below 2 GiB.
+#ifndef RPL_F32_STAGES
+#define RPL_F32_STAGES 4
+#endif
+namespace fd {
+constexpr int BM = 256, BN = 256, BK = 16, S = RPL_F32_STAGES, kThreads = 256;
+constexpr int kTileBytes = BM * BK * 4;  // one operand of one stage: 16 KB
+constexpr int kStageBytes = 2 * kTileBytes;
+constexpr int kLoads = 4;                // 1 KB copies per wave per operand per tile
+constexpr int kVmPerTile = 2 * kLoads;
+static_assert(S >= 3 && S * kStageBytes <= 160 * 1024, "LDS ring must fit 160 KB");
+
+// One operand of the tile: KC = k-contiguous in memory.
+template <bool KC>
+struct Op {
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t voff[kLoads];
+    uint32_t kstep;  // bytes to advance one 16-k tile
+    uint32_t fofs;   // lane's fragment offset within the operand's LDS tile (half 0)
+
+    // X: [rows_total, K] (KC) or [K, rows_total]; r0 = first tile row.
+    __device__ __forceinline__ void init(const float* X, uint32_t ld, uint32_t rows_total, uint32_t K, uint32_t r0,
+                                         uint32_t wave, uint32_t lane, uint32_t wofs) {
+        const uint32_t valid = rows_total - r0 < (uint32_t)BM ? rows_total - r0 : BM;
+        if (KC) {
+            rsrc = uniform_rsrc(X + (uint64_t)r0 * ld, valid * ld * 4);
+#pragma unroll
+            for (int i = 0; i < kLoads; i++) {
+                const uint32_t r = wave * 64 + i * 16 + lane / 4;
+                voff[i] = (r < valid ? r : valid - 1) * ld * 4 + ((lane % 4) ^ swz(r)) * 16;
+            }
+            kstep = BK * 4;
+            const uint32_t fr = lane % 32;
+            fofs = (wofs + fr) * 64 + ((lane / 32) ^ swz(fr)) * 16;
+        } else {
+            rsrc = uniform_rsrc(X + r0, (uint32_t)(((uint64_t)(K - 1) * ld + valid) * 4));
+            const uint32_t c = 4 * lane < valid - 4 ? 4 * lane : valid - 4;
+#pragma unroll
+            for (int i = 0; i < kLoads; i++) voff[i] = (wave * kLoads + i) * ld * 4 + c * 4;
+            kstep = BK * ld * 4;
+            fofs = (4 * (lane / 32)) * (BM * 4) + (wofs + 4 * (lane % 32)) * 4;
+        }
+    }
+
+    __device__ __forceinline__ void issue(uint32_t kt, char* st, uint32_t wave) const {
+#pragma unroll
+        for (int i = 0; i < kLoads; i++) {
+            char* dst = KC ? st + (wave * 64 + i * 16) * 64 : st + (wave * kLoads + i) * (BM * 4);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)dst, 16, voff[i], kt * kstep, 0, 0);
+        }
+    }
+
+    // Fragment registers of half t: KC: x[b] = block b, substeps 0..3;
+    // row-contiguous: x[s] = substep s, blocks 0..3.
+    __device__ __forceinline__ void frags(const char* st, int t, v4f (&x)[4]) const {
+        // KC: chunk l/32 + 2t sits at slot (l/32 ^ swz) ^ 2t, i.e. the half-0
+        // offset with bit 5 flipped (rows are 64-byte aligned).
+        const uint32_t base = KC ? (fofs ^ (32u * t)) : fofs + 8 * t * (BM * 4);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            x[q] = *reinterpret_cast<const v4f*>(st + base + (KC ? q * 32 * 64 : q * (BM * 4)));
+    }
+
+    // Operand of block f at substep s.
+    __device__ __forceinline__ static float val(const v4f (&x)[4], int f, int s) { return KC ? x[f][s] : x[s][f]; }
+
+    // Tile-relative row (within the wave's 128) of block f, block-local row i.
+    __device__ __forceinline__ static uint32_t row(int f, uint32_t i) { return KC ? f * 32 + i : 4 * i + f; }
+};
+}  // namespace fd
+
+template <bool TA, bool TB>
+__global__ void __launch_bounds__(256, 1) k_sgemm_dma(uint32_t M, uint32_t N, uint32_t K, float alpha,
+                                                      const float* __restrict__ A, uint32_t lda,
+                                                      const float* __restrict__ B, uint32_t ldb, float beta,
+                                                      float* __restrict__ C, uint32_t ldc) {
+    using fd::BK;
+    using fd::BM;
+    using fd::BN;
+    using fd::kLoads;
+    using fd::kStageBytes;
+    using fd::kTileBytes;
+    using fd::kVmPerTile;
+    using fd::S;
+    using OpA = fd::Op<!TA>;
+    using OpB = fd::Op<TB>;
+    __shared__ __attribute__((aligned(1024))) char smem[S * kStageBytes];
+
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t wm = wave / 2, wn = wave % 2;
+    uint32_t im, in;
+    rplhip::tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, im, in);
+    const uint32_t m0 = im * BM, n0 = in * BN;
+    OpA opa;
+    OpB opb;
+    opa.init(A, lda, M, K, m0, wave, lane, wm * 128);
+    opb.init(B, ldb, N, K, n0, wave, lane, wn * 128);
+
+    auto issue_a = [&](uint32_t kt, uint32_t stage) { opa.issue(kt, smem + stage * kStageBytes, wave); };
+    auto issue_b = [&](uint32_t kt, uint32_t stage) { opb.issue(kt, smem + stage * kStageBytes + kTileBytes, wave); };
+    auto issue = [&](uint32_t kt, uint32_t stage) {
+        issue_a(kt, stage);
+        issue_b(kt, stage);
+    };
+    // Wait until this wave's copies of tile kt+1 have landed, given that
+    // `later` whole tiles were issued after it.
+    auto wait_after = [&](uint32_t later) {
+        static_for<S - 1>([&](auto Cn) {
+            constexpr int c = decltype(Cn)::value;
+            if (later == (uint32_t)c) __builtin_amdgcn_s_waitcnt(waitcnt_imm(c * kVmPerTile, 0));
+        });
+    };
+    struct F {
+        v4f a[4], b[4];
+    };
+    auto fload = [&](uint32_t stage, int t, F& f) {
+        const char* st = smem + stage * kStageBytes;
+        opa.frags(st, t, f.a);
+        opb.frags(st + kTileBytes, t, f.b);
+    };
+    v16f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = (v16f){};
+    auto mma = [&](const F& f) {
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(OpA::val(f.a, i, s), OpB::val(f.b, j, s),
+                                                                     acc[i][j], 0, 0, 0);
+    };
+    // Pin each half's order: the 8 fragment reads early, one between
+    // MFMA pairs, then the tile copies, so no MFMA waits on a read issued
+    // just before it.
+    auto pin = [&](auto copies) {
+        static_for<8>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        });
+        static_for<decltype(copies)::value>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // HBM -> LDS copy
+        });
+    };
+
+    const uint32_t nk = K / BK;
+    static_for<S - 1>([&](auto T) {
+        constexpr int t = decltype(T)::value;
+        if (t < nk) issue(t, t);
+    });
+    wait_after(nk - 1 < (uint32_t)(S - 2) ? nk - 1 : S - 2);
+    __builtin_amdgcn_s_barrier();
+    F f0, f1;
+    fload(0, 0, f0);
+
+    // Iteration kt: request tile kt+S-1 (A copies in the first half, B in
+    // the second) into the stage tile kt-1 left, read tile kt's second half
+    // while multiplying its first, wait for tile kt+1 and barrier, read tile
+    // kt+1's first half while multiplying kt's second.
+    constexpr int kLaterSteady = (S - 3) * kVmPerTile + kLoads;
+    uint32_t kt = 0;
+    for (; kt + 2 * S - 1 <= nk; kt += S) {
+        static_for<S>([&](auto U) {
+            constexpr int u = decltype(U)::value;
+            __builtin_amdgcn_sched_barrier(0);
+            issue_a(kt + u + S - 1, (u + S - 1) % S);
+            fload(u, 1, f1);
+            mma(f0);
+            pin(std::integral_constant<int, kLoads>{});
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLaterSteady, 0));
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            issue_b(kt + u + S - 1, (u + S - 1) % S);
+            fload((u + 1) % S, 0, f0);
+            mma(f1);
+            pin(std::integral_constant<int, kLoads>{});
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+    for (; kt < nk; kt++) {
+        if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+        fload(kt % S, 1, f1);
+        mma(f0);
+        const uint32_t last = kt + S - 1 < nk - 1 ? kt + S - 1 : nk - 1;
+        wait_after(last > kt + 1 ? last - kt - 1 : 0);
+        __builtin_amdgcn_s_barrier();
+        if (kt + 1 < nk) fload((kt + 1) % S, 0, f0);
+        mma(f1);
+    }
+
+    // Epilogue.  Result register r of lane l in block (i, j) is block-local
+    // row 8(r/4) + 4(l/32) + r%4 and column l%32.
+    const uint32_t mw = m0 + wm * 128, nw = n0 + wn * 128;
+    const bool full = m0 + BM <= M && n0 + BN <= N;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const uint32_t m = mw + OpA::row(i, 8 * (r / 4) + 4 * (lane / 32) + r % 4);
+            if (!full && m >= M) continue;
+            float* crow = C + (uint64_t)m * ldc;
+            if (!TB) {
+                // Interleaved columns: block j holds column 4(l%32) + j.
+                const uint32_t n = nw + 4 * (lane % 32);
+                if (full || n + 3 < N) {
+                    float4* cp = reinterpret_cast<float4*>(crow + n);
+                    float4 c = *cp;
+                    c.x = alpha * acc[i][0][r] + beta * c.x;
+                    c.y = alpha * acc[i][1][r] + beta * c.y;
+                    c.z = alpha * acc[i][2][r] + beta * c.z;
+                    c.w = alpha * acc[i][3][r] + beta * c.w;
+                    *cp = c;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t n = nw + j * 32 + lane % 32;
+                    if (full || n < N) crow[n] = alpha * acc[i][j][r] + beta * crow[n];
+                }
+            }
+        }
+}
+
 // C = alpha * sum_s W[s] + beta * C over the split partials W[s] ([M, N],
 // ld N), summed in split order (deterministic).
 __global__ void __launch_bounds__(256) k_splitk_reduce(const float* __restrict__ W, uint32_t splits, uint32_t M,
@@ -276,6 +540,17 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
     const uint64_t tiles = (uint64_t)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
     if (tiles > 0x7fffffffull) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "sgemm: %u x %u too large", M, N);
     dim3 grid((uint32_t)tiles);
+    // Big grids on the direct-to-LDS kernel (RPLHIP_F32_DMA=0 disables it,
+    // for A/B timing only).
+    static const char* dma_env = getenv("RPLHIP_F32_DMA");
+    const uint64_t big_tiles = (uint64_t)((M + fd::BM - 1) / fd::BM) * ((N + fd::BN - 1) / fd::BN);
+    const uint64_t a_bytes = (uint64_t)(TA ? K : M) * lda * 4, b_bytes = (uint64_t)(TB ? N : K) * ldb * 4;
+    if (vec && K >= fd::BK && K % fd::BK == 0 && big_tiles >= 2ull * rplhip::cu_count() && a_bytes < (1ull << 31) &&
+        b_bytes < (1ull << 31) && !(dma_env && dma_env[0] == '0')) {
+        hipLaunchKernelGGL((k_sgemm_dma<TA, TB>), dim3((uint32_t)big_tiles), dim3(fd::kThreads), 0, s, M, N, K, alpha,
+                           A, lda, B, ldb, beta, C, ldc);
+        return rplhip::check_launch("sgemm (direct-to-LDS)");
+    }
     const uint32_t splits = k_splits(tiles, K);
     if (splits > 1) {
         // Partial tiles into a stream-ordered workspace, then one reduction.

@@ -34,20 +34,16 @@
 
 #include <type_traits>
 
-#include "common.h"
+#include "mfma_pipe.h"
 
 namespace {
 
+using rplhip::lds_ptr;
+using rplhip::static_for;
+using rplhip::swz;
 using rplhip::tile_of;
-
-// Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 at compile time.
-template <int N, int I = 0, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        static_for<N, I + 1>(f);
-    }
-}
+using rplhip::uniform_rsrc;
+using rplhip::waitcnt_imm;
 
 enum Epi { kRaw = 0, kRequant = 1, kDequant = 2, kRequantPow2 = 3 };
 
@@ -159,30 +155,8 @@ __device__ __forceinline__ v4i load_chunk_stream(const int8_t* __restrict__ base
 // steady-state iterations carry no conditions (edge tiles and the last
 // iterations run a separate, checked copy of the loop), which lets the
 // compiler wait only for the loads it needs (vmcnt) instead of draining.
-//
-// LDS rows are unpadded 64-byte k-slices; the four 16-byte chunks of row r
-// are stored XOR-swizzled (chunk c at slot c ^ swz(r)), so both the 128-bit
-// fragment reads (16 consecutive rows, same chunk) and the 128-bit tile
-// writes (4 chunks of consecutive rows) touch distinct banks whether the
-// LDS serves 8 lanes x 16 bytes over 32 banks or 16 lanes over 64 banks.
-__device__ __forceinline__ uint32_t swz(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3; }
-
-// Word 3 of a raw buffer resource on gfx950 (32-bit data format, no
-// swizzle, range-checked against num_records).
-constexpr int kBufferFlags = 0x00020000;
-
-// Raw buffer resource for `bytes` bytes at `base`.  The fields go through
-// readfirstlane so the resource is provably wave-uniform and lives in SGPRs:
-// a resource the compiler cannot prove uniform makes it wrap every buffer
-// load in a readfirstlane/compare/exec loop.  Callers pass values that are
-// uniform already (derived from blockIdx and kernel arguments).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, uint32_t bytes) {
-    const uint64_t p = (uint64_t)(uintptr_t)base;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
-    const uint32_t n = __builtin_amdgcn_readfirstlane(bytes);
-    return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, (int)n, kBufferFlags);
-}
+// LDS rows are unpadded 64-byte k-slices with XOR-swizzled 16-byte chunks
+// (rplhip::swz).
 
 template <int BM_, int BN_>
 struct Cfg {
@@ -506,9 +480,6 @@ __device__ __forceinline__ void epilogue_tile_full(const EpiParams& p, const v16
 
 // ------------------------------------ NT core GEMM, direct-to-LDS pipeline
 
-// gfx9 s_waitcnt immediate: vmcnt in bits [3:0] and [15:14], expcnt [6:4],
-// lgkmcnt [11:8]; a field at its maximum does not wait.
-constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8); }
 
 // Tuning knobs (defaults measured best on MI355X): LDS stages in the ring
 // and where the copies of a tile are issued (0: both operands in the first
@@ -565,7 +536,6 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
                                                            const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
                                                            uint32_t N, uint32_t K, EpiParams p) {
     using namespace dma;
-    typedef __attribute__((address_space(3))) void* lds_ptr;
     __shared__ __attribute__((aligned(1024))) int8_t smem[S * kStageBytes];
 
     const uint32_t lane = threadIdx.x % 64;
@@ -755,7 +725,6 @@ __global__ void __launch_bounds__(512, 1) k_gemm_i8_nt_pp(const int8_t* __restri
                                                           const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
                                                           uint32_t N, uint32_t K, EpiParams p) {
     using namespace pp;
-    typedef __attribute__((address_space(3))) void* lds_ptr;
     __shared__ __attribute__((aligned(1024))) int8_t smem[S * kStageBytes];
 
     const uint32_t lane = threadIdx.x % 64;

@@ -129,6 +129,45 @@ def test_config4_8192_sampled_rows(gpu):
     assert np.max(np.abs(lhs - rhs) / scale) <= fp32_tol(n)
 
 
+# Grids with >= 2 tiles of 256 x 256 per CU take the direct-to-LDS kernel
+# (k_sgemm_dma).  (5900, 5892, 1040): ragged M and N edges, 65 k-tiles (the
+# unrolled steady-state loop plus a 5-tile tail); (6144, 6144, 48): only the
+# tail loop.  All four transposes, alpha/beta, a NaN in C (C is always read).
+@pytest.mark.parametrize("M,N,K", [(5900, 5892, 1040), (6144, 6144, 48)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_big_tile_paths(gpu, M, N, K, ta, tb):
+    rng = np.random.default_rng(M + N + K + 2 * ta + tb)
+    A = rng.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (N, K) if tb else (K, N)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+    C0[M // 2, N // 3] = np.nan
+    alpha, beta = 0.75, -0.5
+    say("sgemm big tile", M, N, K, ta, tb)
+    out = sgemm(A, B, C0, M, N, K, alpha, beta, ta, tb)
+    opA, opB = op(A, ta).astype(np.float64), op(B, tb).astype(np.float64)
+    assert np.isnan(out[M // 2, N // 3]) and np.isnan(out).sum() == 1
+    rows = np.unique(np.concatenate([[0, M - 1, M // 2], rng.choice(M, 12, replace=False)]))
+    ref = alpha * (opA[rows] @ opB) + beta * C0[rows].astype(np.float64)
+    denom = abs(alpha) * (np.abs(opA[rows]) @ np.abs(opB)) + abs(beta) * np.abs(C0[rows].astype(np.float64))
+    ok = ~np.isnan(ref)
+    assert np.max(np.abs(out[rows] - ref)[ok] / denom[ok]) <= fp32_tol(K)
+    # Every row and column through C x = alpha A (B x) + beta C0 x (NaN column dropped).
+    x = rng.standard_normal(N)
+    x[N // 3] = 0.0
+    c0 = np.nan_to_num(C0.astype(np.float64))
+    o = np.nan_to_num(out.astype(np.float64))
+    lhs = o @ x
+    rhs = alpha * (opA @ (opB @ x)) + beta * (c0 @ x)
+    scale = abs(alpha) * (np.abs(opA) @ (np.abs(opB) @ np.abs(x))) + abs(beta) * (np.abs(c0) @ np.abs(x))
+    assert np.max(np.abs(lhs - rhs) / scale) <= fp32_tol(K)
+    y = rng.standard_normal(M)
+    y[M // 2] = 0.0
+    lhs = y @ o
+    rhs = alpha * ((y @ opA) @ opB) + beta * (y @ c0)
+    scale = abs(alpha) * ((np.abs(y) @ np.abs(opA)) @ np.abs(opB)) + abs(beta) * (np.abs(y) @ np.abs(c0))
+    assert np.max(np.abs(lhs - rhs) / scale) <= fp32_tol(K)
+
+
 # ---------------------------------------------------- through include/rpl.h
 
 def tensor_from(lib, arr, requires_grad=False):
