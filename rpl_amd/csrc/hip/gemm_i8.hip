@@ -1175,6 +1175,71 @@ __global__ void __launch_bounds__(256) k_transpose_i8(const int8_t* __restrict__
     }
 }
 
+// B [K,N] -> Bt [N,K] for whole 128 x 128 tiles (K, N multiples of 128,
+// 16-byte aligned).  Loads move whole 128-byte rows of B into LDS (row
+// pitch 144 bytes); the byte transpose is done by ds_read_b64_tr_b8: in each
+// group of 16 lanes, output lane 8h+b receives as byte e the byte b of the
+// 8-byte piece addressed by lane 2e+h.  Lane 2e+h addresses k-row kb+e at
+// column nb+8h, so output lane i gets column nb+i for k-rows kb..kb+7, and
+// two reads give it 16 consecutive k-bytes of one column.  Those pieces go
+// through the LDS tile again, laid out [n][k], so that the stores write whole
+// 128-byte rows of Bt (8 lanes per row): stored straight from the transposed
+// reads, every store instruction would touch 64 rows with 16 bytes each,
+// and the L2 request rate, not HBM, would set the speed.  Both layouts use a
+// 144-byte pitch: the 8 k-rows of a transposed read, and the 16 n-rows a
+// lane group writes, fall on distinct LDS banks.
+constexpr int kTrTile = 128, kTrPitch = 144;
+__global__ void __launch_bounds__(256) k_transpose_i8_tr(const int8_t* __restrict__ B, uint32_t K, uint32_t N,
+                                                         int8_t* __restrict__ Bt) {
+    // One tile, [k][n] then [n][k]: 18 KB, so 8 blocks fit a CU and keep
+    // ~128 KB of loads in flight per CU.
+    __shared__ __attribute__((aligned(16))) int8_t s[kTrTile * kTrPitch];
+    // Diagonal block order: blocks that run together differ in both n0 (the
+    // load side's column) and k0 (the store side's column), so neither side
+    // walks one column of rows 8 KB apart.
+    const uint32_t nx = N / kTrTile, ny = K / kTrTile, b = blockIdx.x;
+    const uint32_t bx = b % nx, by = (b / nx + bx) % ny;
+    const uint32_t k0 = by * kTrTile, n0 = bx * kTrTile;
+    const uint32_t t = threadIdx.x, lane = t % 64, wave = t / 64;
+    v4i v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t row = 32 * i + t / 8, chunk = t % 8;
+        v[i] = *reinterpret_cast<const v4i*>(B + (uint64_t)(k0 + row) * N + n0 + 16 * chunk);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t row = 32 * i + t / 8, chunk = t % 8;
+        *reinterpret_cast<v4i*>(s + row * kTrPitch + 16 * chunk) = v[i];
+    }
+    __syncthreads();
+    typedef __attribute__((address_space(3))) v2i* lds_v2i;
+    const uint32_t g = lane / 16, i = lane % 16;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint32_t idx = wave * 4 + q;
+        const uint32_t nb = 64 * (idx % 2) + 16 * g, kb = 16 * (idx / 2);
+        const int8_t* a = s + (kb + i / 2) * kTrPitch + nb + 8 * (i % 2);
+        const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i)a);
+        const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i)(a + 8 * kTrPitch));
+        v[q] = (v4i){lo.x, lo.y, hi.x, hi.y};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint32_t idx = wave * 4 + q;
+        const uint32_t nb = 64 * (idx % 2) + 16 * g, kb = 16 * (idx / 2);
+        *reinterpret_cast<v4i*>(s + (nb + i) * kTrPitch + kb) = v[q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i2 = 0; i2 < 4; i2++) {
+        const uint32_t row = 32 * i2 + t / 8, chunk = t % 8;
+        *reinterpret_cast<v4i*>(Bt + (uint64_t)(n0 + row) * K + k0 + 16 * chunk) =
+            *reinterpret_cast<const v4i*>(s + row * kTrPitch + 16 * chunk);
+    }
+}
+
 // rowsum[r] = sum_k X[r][k] (int32) for the zero-point correction.
 __global__ void __launch_bounds__(256) k_rowsum_i8(const int8_t* __restrict__ X, uint32_t rows, uint32_t K,
                                                    int32_t* __restrict__ out) {
@@ -1313,6 +1378,11 @@ bool exact_reciprocal(float sc, float* inv) {
 }
 
 int transpose_b(const int8_t* B, uint32_t K, uint32_t N, int8_t* Bt, hipStream_t s) {
+    const uint64_t tr_tiles = (uint64_t)(N / kTrTile) * (K / kTrTile);
+    if (K % kTrTile == 0 && N % kTrTile == 0 && aligned16(B) && aligned16(Bt) && tr_tiles <= 0x7fffffffull) {
+        hipLaunchKernelGGL(k_transpose_i8_tr, dim3((uint32_t)tr_tiles), dim3(256), 0, s, B, K, N, Bt);
+        return rplhip::check_launch("int8 transpose");
+    }
     dim3 grid((N + 63) / 64, (K + 63) / 64);
     if (grid.y > 65535) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "int8 transpose: K=%u too large", K);
     hipLaunchKernelGGL(k_transpose_i8, grid, dim3(256), 0, s, B, K, N, Bt);

@@ -36,8 +36,11 @@ def test_gemm_int8_rpl_api(gpu, golden):
     assert bits_equal(out, golden["i8_zp_C"])
 
 
+# K and N multiples of 128 (256x256x512, 200x384x256, 16x1280x896,
+# 3x128x8192) transpose B with whole 128x128 tiles (k_transpose_i8_tr); the
+# others take the bounds-checked transpose.
 SHAPES = [(1, 1, 1), (4, 9, 16), (16, 100, 64), (17, 31, 300), (129, 127, 129), (256, 256, 512), (64, 8, 1000),
-          (5, 300, 4096)]
+          (5, 300, 4096), (200, 384, 256), (16, 1280, 896), (3, 128, 8192)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
