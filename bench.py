@@ -189,6 +189,27 @@ def bench_configs(lib, stream, timer, steps, with_cpu):
         b = np.zeros(H, np.float32), np.zeros(O, np.float32)
         e["cpu_ms"] = round(_cpu_ms(lambda: orc.mlp_step(X, Y, W1, b[0], W2, b[1])), 1)
     out["cfg2_mlp_step_b4096"] = e
+
+    # The same step followed by optimizer_sgd_step (momentum 0.9) on the
+    # device: a whole training iteration with no host round trip.
+    arr = (C.POINTER(rpl_amd.Tensor) * 4)(*params)
+    opt = lib.optimizer_sgd_create(arr, 4, 0.05, 0.9, 0.0, 0.0, False)
+
+    def cfg2_sgd():
+        cfg2()
+        lib.optimizer_sgd_step(opt)
+
+    for _ in range(3):
+        cfg2_sgd()
+    lib.rpl_gpu_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        cfg2_sgd()
+    lib.rpl_gpu_synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    err = lib.rpl_last_error()
+    out["cfg2_mlp_step_sgd_b4096"] = {"us": round(ms * 1e3, 1), "timing": "host clock, synced",
+                                      "error": err.decode() if err else None}
     for layer in (l1, l2):
         lib.linear_free(layer)
     lib.tensor_free(tX)
@@ -314,6 +335,25 @@ def main():
         sw = DeviceBuffer.from_array(np.full(N, scales[1], np.float32))
         sx = DeviceBuffer.from_array(np.float32([scales[0]]))
         Y = DeviceBuffer(16 * N * 4)
+        # Measured device-to-device copy rate on the same rotation of
+        # buffers (bytes read + written), the practical HBM ceiling.
+        cp = [0]
+
+        def copy():
+            src, dst = Ws[cp[0] % nw], Ws[(cp[0] + 1) % nw]
+            cp[0] += 1
+            check(lib.rplhip_memcpy_dtod(dst.ptr, src.ptr, N * K, stream))
+
+        ms_c, _ = timer.time(copy, 30, 5)
+        copy_gbs = 2 * N * K / (ms_c * 1e-3) / 1e9
+        skinny["copy"] = {"GB/s": round(copy_gbs, 1), "frac_hbm": round(copy_gbs / PEAK_HBM_GBS, 3),
+                          "what": "hipMemcpyAsync device-to-device, 64 MiB, read + written bytes"}
+        orc = None
+        if not args.no_cpu:
+            from oracle import Oracle
+            orc = Oracle()
+            qw_host = qB.to_array(np.int8, (N, K))
+            qa_host = qA.to_array(np.int8, (16, K))
         for M in (1, 4, 16):
             it = [0]
 
@@ -324,8 +364,19 @@ def main():
 
             ms_s, _ = timer.time(sk, 60, 12)
             byts = N * K + M * K + M * N * 4 + N * 4 + 4
-            skinny[f"M{M}"] = {"us": round(ms_s * 1e3, 2), "GB/s": round(byts / (ms_s * 1e-3) / 1e9, 1),
-                               "frac_hbm": round(byts / (ms_s * 1e-3) / 1e9 / PEAK_HBM_GBS, 3)}
+            gbs = byts / (ms_s * 1e-3) / 1e9
+            skinny[f"M{M}"] = {"us": round(ms_s * 1e3, 2), "GB/s": round(gbs, 1),
+                               "frac_hbm": round(gbs / PEAK_HBM_GBS, 3), "frac_copy": round(gbs / copy_gbs, 3)}
+            if orc is not None:
+                # The reference's CPU path on the same shape: linear_int8
+                # (rpl_quantization.c:314-353) then the dequant.
+                swh = np.full(N, scales[1], np.float32)
+
+                def cpu_sk():
+                    acc = orc.linear_int8(np.ascontiguousarray(qa_host[:M]), qw_host, None, M, K, N)
+                    orc.dequant_acc(acc, np.float32([scales[0]]), False, swh, True)
+
+                skinny[f"M{M}"]["cpu_ms"] = round(_cpu_ms(cpu_sk), 2)
         del Ws
 
     configs = None

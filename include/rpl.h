@@ -159,6 +159,24 @@ Linear* linear_create(uint32_t in_features, uint32_t out_features);
 Tensor* linear_forward(Linear* layer, const Tensor* input);
 void linear_free(Linear* layer);
 
+/* ---- SGD optimizer step on the device (include/rpl.h:306-316,
+ * src/rpl_training.c:20-114).  Optimizer is opaque; its layout is the
+ * reference's, so optimizers made by either library interoperate with the
+ * reference's optimizer_step / optimizer_free / schedulers. ---- */
+typedef enum {
+    OPTIMIZER_SGD,
+    OPTIMIZER_ADAM,
+    OPTIMIZER_RMSPROP,
+    OPTIMIZER_ADAGRAD,
+    OPTIMIZER_ADAMW,
+    OPTIMIZER_LAMB
+} OptimizerType;
+typedef struct Optimizer Optimizer;
+Optimizer* optimizer_sgd_create(Tensor** parameters, uint32_t num_params, float lr, float momentum,
+                                float dampening, float weight_decay, bool nesterov);
+/* src/rpl_training.c:70-114 (exported there, called by optimizer_step). */
+void optimizer_sgd_step(Optimizer* opt);
+
 /* ---- additions of this backend (no reference counterpart) ---- */
 /* Reason for the last failure on this thread ("" if none). */
 const char* rpl_last_error(void);

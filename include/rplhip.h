@@ -182,6 +182,12 @@ int rplhip_mse_loss(const float* pred, const float* target, uint64_t n, float* l
  * g0 read from the DEVICE float *g0. */
 int rplhip_mse_backward(const float* pred, const float* target, uint64_t n, const float* g0,
                         float* dpred, rplhip_stream_t stream);
+/* optimizer_sgd_step (src/rpl_training.c:70-114) on one parameter tensor of
+ * n floats, all DEVICE pointers: weight decay and Nesterov update grad in
+ * place as the reference does; velocity (the momentum buffer) may be NULL
+ * when momentum == 0. */
+int rplhip_sgd_step(float* param, float* grad, float* velocity, uint64_t n, float lr, float momentum,
+                    float dampening, float weight_decay, int nesterov, rplhip_stream_t stream);
 /* Fill a DEVICE float buffer with a value (tensor_fill, src/rpl_core.c:83-86). */
 int rplhip_fill(float* x, uint64_t n, float value, rplhip_stream_t stream);
 

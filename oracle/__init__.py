@@ -40,6 +40,7 @@ PROTOTYPES = {
     "orc_mse_loss": (_f32, [_vp, _vp, _u32]),
     "orc_mse_backward": (None, [_vp, _vp, _u32, _f32, _vp]),
     "orc_mlp_step": (_f32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32] + [_vp] * 7),
+    "orc_sgd_step": (None, [_vp, _vp, _vp, _u32, _f32, _f32, _f32, _f32, _b]),
 }
 
 
@@ -195,6 +196,12 @@ class Oracle:
         self.lib.orc_mse_backward(_p(np.ascontiguousarray(p, np.float32)), _p(np.ascontiguousarray(t, np.float32)),
                                   dp.size, g0, _p(dp))
         return dp
+
+    def sgd_step(self, p, g, v, lr, momentum, dampening, weight_decay, nesterov):
+        """One optimizer_sgd_step on one parameter tensor, in place on p, g, v
+        (float32 arrays); v may be None when momentum == 0."""
+        v = v if v is not None else np.zeros(1, np.float32)
+        self.lib.orc_sgd_step(_p(p), _p(g), _p(v), p.size, lr, momentum, dampening, weight_decay, bool(nesterov))
 
     def mlp_step(self, X, Y, W1, b1, W2, b2):
         X, Y, W1, b1, W2, b2 = (np.ascontiguousarray(v, np.float32) for v in (X, Y, W1, b1, W2, b2))

@@ -339,3 +339,27 @@ float orc_mlp_step(const float* X, const float* Y, const float* W1, const float*
     free(mm1); free(mm2); free(g_out2); free(g_mm2); free(g_a); free(g_out1); free(g_mm1);
     return loss;
 }
+
+/* rpl_training.c:70-114 (optimizer_sgd_step) for one parameter tensor: the
+ * same loops and expression shapes, so GCC forms the same FMAs.  grad is
+ * updated in place (weight decay, Nesterov), as in the reference. */
+void orc_sgd_step(float* param, float* grad, float* velocity, uint32_t n, float lr, float momentum,
+                  float dampening, float weight_decay, bool nesterov) {
+    float* d_p = grad;
+    if (weight_decay != 0.0f) {
+#pragma omp simd
+        for (uint32_t i = 0; i < n; i++) d_p[i] += weight_decay * param[i];
+    }
+    if (momentum != 0.0f) {
+#pragma omp simd
+        for (uint32_t i = 0; i < n; i++) velocity[i] = momentum * velocity[i] + (1.0f - dampening) * d_p[i];
+        if (nesterov) {
+#pragma omp simd
+            for (uint32_t i = 0; i < n; i++) d_p[i] += momentum * velocity[i];
+        } else {
+            d_p = velocity;
+        }
+    }
+#pragma omp simd
+    for (uint32_t i = 0; i < n; i++) param[i] -= lr * d_p[i];
+}

@@ -117,6 +117,10 @@ float orc_mlp_step(const float* X, const float* Y, const float* W1, const float*
                    uint32_t O, float* h, float* a, float* o, float* dW1, float* db1,
                    float* dW2, float* db2);
 
+/* rpl_training.c:70-114 */
+void orc_sgd_step(float* param, float* grad, float* velocity, uint32_t n, float lr, float momentum,
+                  float dampening, float weight_decay, bool nesterov);
+
 #ifdef __cplusplus
 }
 #endif

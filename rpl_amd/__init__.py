@@ -108,6 +108,30 @@ class Linear(C.Structure):
     ]
 
 
+class Optimizer(C.Structure):
+    """Reference src/rpl_training.c:20-28 (opaque in include/rpl.h)."""
+
+    _fields_ = [
+        ("type", C.c_int),
+        ("learning_rate", C.c_float),
+        ("weight_decay", C.c_float),
+        ("num_params", C.c_uint32),
+        ("parameters", C.POINTER(C.POINTER(Tensor))),
+        ("state", C.c_void_p),
+    ]
+
+
+class SGDState(C.Structure):
+    """Reference src/rpl_training.c:34-39."""
+
+    _fields_ = [
+        ("momentum", C.c_float),
+        ("dampening", C.c_float),
+        ("nesterov", C.c_bool),
+        ("velocity", C.POINTER(C.POINTER(Tensor))),
+    ]
+
+
 _vp, _u32, _u64, _i32, _f32, _int, _sz = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int32, C.c_float, C.c_int, C.c_size_t
 _PT, _PQ = C.POINTER(Tensor), C.POINTER(QuantizedTensor)
 _fp, _i8p, _i32p = C.POINTER(C.c_float), C.POINTER(C.c_int8), C.POINTER(C.c_int32)
@@ -153,6 +177,7 @@ PROTOTYPES = {
     "rplhip_bias_grad": (_int, [_vp, _u64, _vp, _u64, _vp]),
     "rplhip_mse_loss": (_int, [_vp, _vp, _u64, _vp, _vp]),
     "rplhip_mse_backward": (_int, [_vp, _vp, _u64, _vp, _vp, _vp]),
+    "rplhip_sgd_step": (_int, [_vp, _vp, _vp, _u64, _f32, _f32, _f32, _f32, _int, _vp]),
     "rplhip_fill": (_int, [_vp, _u64, _f32, _vp]),
     # ---- rpl.h
     "tensor_create": (_PT, [_u32, C.POINTER(_u32), C.c_bool]),
@@ -200,6 +225,8 @@ PROTOTYPES = {
     "linear_create": (C.POINTER(Linear), [_u32, _u32]),
     "linear_forward": (_PT, [C.POINTER(Linear), _PT]),
     "linear_free": (None, [C.POINTER(Linear)]),
+    "optimizer_sgd_create": (C.POINTER(Optimizer), [C.POINTER(_PT), _u32, _f32, _f32, _f32, _f32, C.c_bool]),
+    "optimizer_sgd_step": (None, [C.POINTER(Optimizer)]),
     "rpl_last_error": (C.c_char_p, []),
     "rpl_gpu_synchronize": (None, []),
     "rpl_gpu_stream": (_vp, []),

@@ -139,6 +139,38 @@ __global__ void __launch_bounds__(kThreads) k_mse_backward(const float* __restri
     GRID_STRIDE(i, n) { dp[i] += g0 * factor * (p[i] - t[i]); }
 }
 
+// optimizer_sgd_step (src/rpl_training.c:70-114), one element per thread.
+// The reference's loops compile (GCC -O3, FMA) to these fused forms, which
+// the oracle's golden vectors pin bit for bit:
+//   g = fma(wd, p, g)                   weight decay (grad updated in place)
+//   v = fma(mom, v, (1 - damp) * g)     momentum buffer
+//   g = fma(mom, v, g)                  Nesterov (grad updated in place)
+//   p = fma(-lr, d, p)                  d = g (Nesterov / no momentum) or v
+__global__ void __launch_bounds__(kThreads) k_sgd_step(float* __restrict__ p, float* __restrict__ g,
+                                                       float* __restrict__ v, uint64_t n, float lr, float mom,
+                                                       float damp, float wd, int nesterov) {
+#pragma clang fp contract(off)
+    const float keep = 1.0f - damp;
+    GRID_STRIDE(i, n) {
+        const float pi = p[i];
+        float gi = g[i];
+        if (wd != 0.0f) gi = __fmaf_rn(wd, pi, gi);
+        float d = gi;
+        if (mom != 0.0f) {
+            const float vi = __fmaf_rn(mom, v[i], keep * gi);
+            v[i] = vi;
+            if (nesterov) {
+                gi = __fmaf_rn(mom, vi, gi);
+                d = gi;
+            } else {
+                d = vi;
+            }
+        }
+        g[i] = gi;
+        p[i] = __fmaf_rn(-lr, d, pi);
+    }
+}
+
 }  // namespace
 
 using namespace rplhip;
@@ -256,6 +288,16 @@ int rplhip_mse_backward(const float* pred, const float* target, uint64_t n, cons
     hipLaunchKernelGGL(k_mse_backward, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), pred,
                        target, n, g0, dpred);
     return check_launch("mse_backward");
+}
+
+int rplhip_sgd_step(float* param, float* grad, float* velocity, uint64_t n, float lr, float momentum,
+                    float dampening, float weight_decay, int nesterov, rplhip_stream_t stream) {
+    if (n == 0) return RPLHIP_OK;
+    NEED(param && grad && (momentum == 0.0f || velocity), "rplhip_sgd_step");
+    RPLHIP_REQUIRE_DEVICE();
+    hipLaunchKernelGGL(k_sgd_step, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), param, grad, velocity, n,
+                       lr, momentum, dampening, weight_decay, nesterov);
+    return check_launch("sgd_step");
 }
 
 }  // extern "C"

@@ -2,7 +2,8 @@
 
 Runs only where /root/reference is mounted: `make -C oracle ref` compiles the
 reference's hot-path files (src/rpl_core.c, ops_extended.c,
-rpl_quantization.c, rpl_nn.c, gemm_optimized.c) into oracle/_ref/libref.so,
+rpl_quantization.c, rpl_nn.c, gemm_optimized.c, rpl_training.c) into
+oracle/_ref/libref.so,
 and this script calls them through ctypes on seeded inputs, recording inputs
 and outputs.  The committed .npz is pure data (numpy arrays, no pickles);
 tests/test_oracle.py checks the C restatement in oracle/ against it
@@ -25,7 +26,8 @@ REPO = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, REPO)
 
 import rpl_amd  # noqa: E402  (host-side generator + struct layouts only)
-from rpl_amd import Linear, PerChannelQuantizedTensor, QuantizationCalibrator, QuantizedTensor, Tensor  # noqa: E402
+from rpl_amd import (Linear, Optimizer, PerChannelQuantizedTensor, QuantizationCalibrator, QuantizedTensor,  # noqa: E402
+                     SGDState, Tensor)
 from oracle import REF_PATH  # noqa: E402
 
 SEED_BASE = 0x52504C00  # seed(config, stream) = SEED_BASE + 16*config + stream
@@ -64,6 +66,8 @@ def load_ref():
         "tensor_mse_loss": (PT, [PT, PT]),
         "tensor_backward": (None, [PT]),
         "parallel_gemm_optimized": (None, [C.c_void_p, C.c_void_p, C.c_void_p, u32, u32, u32]),
+        "optimizer_sgd_create": (C.POINTER(Optimizer), [C.POINTER(PT), u32, f32, f32, f32, f32, b]),
+        "optimizer_sgd_step": (None, [C.POINTER(Optimizer)]),
     }
     for n, (r, a) in protos.items():
         f = getattr(lib, n)
@@ -315,6 +319,32 @@ def main():
     g["bmm_A"], g["bmm_B"] = A, Bm
     g["bmm_out"] = ref.data(out).reshape(2, 2)
     g["bmm_dA"], g["bmm_dB"] = ref.grad(tA).reshape(2, 2), ref.grad(tB).reshape(2, 2)
+
+    # ---- optimizer_sgd_step (rpl_training.c:70-114): two parameter tensors,
+    # two steps each; grad is modified in place (weight decay, Nesterov).
+    rng = np.random.default_rng(seed(5, 0))
+    shapes = [(37, 53), (53,)]
+    cases = {"plain": (0.1, 0.0, 0.0, 0.0, False), "wd": (0.05, 0.0, 0.0, 1e-2, False),
+             "mom": (0.03, 0.9, 0.0, 0.0, False), "nest": (0.02, 0.9, 0.1, 5e-4, True)}
+    for name, (lr, mom, damp, wd, nest) in cases.items():
+        ps = [ref.tensor(rng.uniform(-1, 1, s).astype(np.float32), requires_grad=True) for s in shapes]
+        arr = (C.POINTER(Tensor) * len(ps))(*ps)
+        opt = L.optimizer_sgd_create(arr, len(ps), lr, mom, damp, wd, nest)
+        for k, t in enumerate(ps):
+            g[f"sgd_{name}_p{k}_init"] = ref.data(t)
+        for step in range(2):
+            for k, t in enumerate(ps):
+                gr = (rng.standard_normal(t.contents.size) * 0.1).astype(np.float32)
+                C.memmove(t.contents.grad, gr.ctypes.data, gr.nbytes)
+                g[f"sgd_{name}_s{step}_g{k}_in"] = gr
+            L.optimizer_sgd_step(opt)
+            st = C.cast(opt.contents.state, C.POINTER(SGDState)).contents
+            for k, t in enumerate(ps):
+                g[f"sgd_{name}_s{step}_p{k}"] = ref.data(t)
+                g[f"sgd_{name}_s{step}_g{k}"] = ref.grad(t)
+                if mom:
+                    g[f"sgd_{name}_s{step}_v{k}"] = ref.data(st.velocity[k])
+        g[f"sgd_{name}_hyper"] = np.array([lr, mom, damp, wd, float(nest)], np.float32)
 
     # ---- configs 0 and 1 at 512^3: hashes of the reference outputs
     n = 512

@@ -47,6 +47,12 @@ def test_struct_layouts_match_reference():
     assert C.sizeof(T) == 152
     assert C.sizeof(rpl_amd.QuantizedTensor) == 56
     assert C.sizeof(rpl_amd.PerChannelQuantizedTensor) == 72
+    # src/rpl_training.c:20-39 (the SGD golden vectors read the reference's
+    # momentum buffers through these layouts).
+    O, S = rpl_amd.Optimizer, rpl_amd.SGDState
+    assert (O.learning_rate.offset, O.weight_decay.offset, O.num_params.offset, O.parameters.offset,
+            O.state.offset, C.sizeof(O)) == (4, 8, 12, 16, 24, 32)
+    assert (S.dampening.offset, S.nesterov.offset, S.velocity.offset, C.sizeof(S)) == (4, 8, 16, 24)
 
 
 def test_no_device_fails_loudly(rpl):

@@ -304,3 +304,41 @@ def test_mlp_step_finite_differences(orc):
             args[name][idx] -= 2 * eps
             lm = loss64(**args)
             assert abs((lp - lm) / (2 * eps) - dP[idx]) < 1e-3, (name, idx)
+
+
+@pytest.mark.parametrize("name", ["plain", "wd", "mom", "nest"])
+def test_sgd_step_golden(orc, golden, name):
+    # optimizer_sgd_step (rpl_training.c:70-114) replayed on the reference
+    # build's inputs: parameters, in-place gradients and velocities after
+    # each of two steps, bit for bit.
+    lr, mom, damp, wd, nest = (float(x) for x in golden[f"sgd_{name}_hyper"])
+    for k in range(2):
+        p = golden[f"sgd_{name}_p{k}_init"].copy()
+        v = np.zeros_like(p)
+        for step in range(2):
+            g = golden[f"sgd_{name}_s{step}_g{k}_in"].copy()
+            orc.sgd_step(p, g, v if mom else None, lr, mom, damp, wd, bool(nest))
+            assert bits_equal(p, golden[f"sgd_{name}_s{step}_p{k}"]), (name, k, step)
+            assert bits_equal(g, golden[f"sgd_{name}_s{step}_g{k}"]), (name, k, step)
+            if mom:
+                assert bits_equal(v, golden[f"sgd_{name}_s{step}_v{k}"]), (name, k, step)
+
+
+def test_sgd_step_closed_forms(orc):
+    # Mathematics, not the formula again: plain SGD is p - lr*g rounded once
+    # (within one float32 ulp of the float64 value); from v = 0 with no
+    # dampening, one momentum step leaves v == g exactly and moves p exactly
+    # like plain SGD; weight decay with g = 0 makes g == wd*p (one rounding).
+    rng = np.random.default_rng(5)
+    p0 = rng.uniform(-1, 1, 4096).astype(np.float32)
+    g0 = (rng.standard_normal(4096) * 0.1).astype(np.float32)
+    p, g = p0.copy(), g0.copy()
+    orc.sgd_step(p, g, None, 0.03, 0.0, 0.0, 0.0, False)
+    exact = p0.astype(np.float64) - np.float64(np.float32(0.03)) * g0.astype(np.float64)
+    assert np.max(np.abs(p - exact) / np.spacing(np.abs(exact).astype(np.float32))) <= 1.0
+    pm, gm, v = p0.copy(), g0.copy(), np.zeros_like(p0)
+    orc.sgd_step(pm, gm, v, 0.03, 0.9, 0.0, 0.0, False)
+    assert bits_equal(v, g0) and bits_equal(pm, p)
+    pw, gw = p0.copy(), np.zeros_like(p0)
+    orc.sgd_step(pw, gw, None, 0.0, 0.0, 0.0, 0.25, False)
+    assert bits_equal(gw, (np.float32(0.25) * p0).astype(np.float32)) and bits_equal(pw, p0)
