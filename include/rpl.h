@@ -110,6 +110,11 @@ void tensor_from_gpu(Tensor* t); /* download data (and grad); stays GPU-resident
 void tensor_add_gpu(Tensor* out, const Tensor* a, const Tensor* b);
 void tensor_matmul_gpu(Tensor* C, const Tensor* A, const Tensor* B);
 void tensor_relu_gpu(Tensor* out, const Tensor* in);
+/* include/rpl.h:112-114: elementwise on the device; an output that is not
+ * resident takes in's shape (its host buffer must hold in->size floats). */
+void tensor_sigmoid_gpu(Tensor* out, const Tensor* in);
+void tensor_tanh_gpu(Tensor* out, const Tensor* in);
+void tensor_gelu_gpu(Tensor* out, const Tensor* in);
 
 /* ---- FP32 GEMM ---- */
 /* include/rpl.h:130, src/rpl_core.c:199-217 */
@@ -180,6 +185,8 @@ void optimizer_sgd_step(Optimizer* opt);
 /* ---- additions of this backend (no reference counterpart) ---- */
 /* Reason for the last failure on this thread ("" if none). */
 const char* rpl_last_error(void);
+/* Forget the recorded failure (rpl_last_error() returns "" again). */
+void rpl_clear_last_error(void);
 /* Wait for all queued device work of this library. */
 void rpl_gpu_synchronize(void);
 /* The library's HIP stream (a hipStream_t), for callers that mix in their

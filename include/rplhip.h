@@ -182,6 +182,14 @@ int rplhip_mse_loss(const float* pred, const float* target, uint64_t n, float* l
  * g0 read from the DEVICE float *g0. */
 int rplhip_mse_backward(const float* pred, const float* target, uint64_t n, const float* g0,
                         float* dpred, rplhip_stream_t stream);
+/* y = activation(x) elementwise, DEVICE pointers (the device seam's
+ * tensor_sigmoid_gpu / tensor_tanh_gpu / tensor_gelu_gpu, src/rpl_gpu.c:
+ * 437-522, with the CPU formulas of src/rpl_core.c:302-304 and 490-497):
+ * sigmoid 1/(1+exp(-x)); tanh; gelu 0.5x(1+tanh(sqrt(2/pi)(x+0.044715x^3))).
+ * Within a few float32 ulp of glibc (the device's exp/tanh/pow differ). */
+int rplhip_sigmoid(const float* x, float* y, uint64_t n, rplhip_stream_t stream);
+int rplhip_tanh(const float* x, float* y, uint64_t n, rplhip_stream_t stream);
+int rplhip_gelu(const float* x, float* y, uint64_t n, rplhip_stream_t stream);
 /* optimizer_sgd_step (src/rpl_training.c:70-114) on one parameter tensor of
  * n floats, all DEVICE pointers: weight decay and Nesterov update grad in
  * place as the reference does; velocity (the momentum buffer) may be NULL

@@ -41,6 +41,9 @@ PROTOTYPES = {
     "orc_mse_backward": (None, [_vp, _vp, _u32, _f32, _vp]),
     "orc_mlp_step": (_f32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32] + [_vp] * 7),
     "orc_sgd_step": (None, [_vp, _vp, _vp, _u32, _f32, _f32, _f32, _f32, _b]),
+    "orc_sigmoid": (None, [_vp, _vp, _u32]),
+    "orc_tanh": (None, [_vp, _vp, _u32]),
+    "orc_gelu": (None, [_vp, _vp, _u32]),
 }
 
 
@@ -202,6 +205,13 @@ class Oracle:
         (float32 arrays); v may be None when momentum == 0."""
         v = v if v is not None else np.zeros(1, np.float32)
         self.lib.orc_sgd_step(_p(p), _p(g), _p(v), p.size, lr, momentum, dampening, weight_decay, bool(nesterov))
+
+    def activation(self, kind, x):
+        """kind in {"sigmoid", "tanh", "gelu"}: the reference's CPU formula."""
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        getattr(self.lib, f"orc_{kind}")(_p(x), _p(y), x.size)
+        return y
 
     def mlp_step(self, X, Y, W1, b1, W2, b2):
         X, Y, W1, b1, W2, b2 = (np.ascontiguousarray(v, np.float32) for v in (X, Y, W1, b1, W2, b2))

@@ -363,3 +363,21 @@ void orc_sgd_step(float* param, float* grad, float* velocity, uint32_t n, float 
 #pragma omp simd
     for (uint32_t i = 0; i < n; i++) param[i] -= lr * d_p[i];
 }
+
+/* tensor_sigmoid (rpl_core.c:302-304) */
+void orc_sigmoid(const float* x, float* y, uint32_t n) {
+    for (uint32_t i = 0; i < n; i++) y[i] = 1.0f / (1.0f + expf(-x[i]));
+}
+
+/* tensor_tanh_inplace (rpl_core.c:490-491), out of place */
+void orc_tanh(const float* x, float* y, uint32_t n) {
+    for (uint32_t i = 0; i < n; i++) y[i] = tanhf(x[i]);
+}
+
+/* tensor_gelu_inplace (rpl_core.c:493-497), out of place */
+void orc_gelu(const float* x, float* y, uint32_t n) {
+    for (uint32_t i = 0; i < n; i++) {
+        float v = x[i];
+        y[i] = 0.5f * v * (1.0f + tanhf(sqrtf(2.0f / M_PI) * (v + 0.044715f * powf(v, 3))));
+    }
+}

@@ -121,6 +121,11 @@ float orc_mlp_step(const float* X, const float* Y, const float* W1, const float*
 void orc_sgd_step(float* param, float* grad, float* velocity, uint32_t n, float lr, float momentum,
                   float dampening, float weight_decay, bool nesterov);
 
+/* rpl_core.c:302-304, 490-497 */
+void orc_sigmoid(const float* x, float* y, uint32_t n);
+void orc_tanh(const float* x, float* y, uint32_t n);
+void orc_gelu(const float* x, float* y, uint32_t n);
+
 #ifdef __cplusplus
 }
 #endif

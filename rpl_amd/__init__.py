@@ -178,6 +178,9 @@ PROTOTYPES = {
     "rplhip_mse_loss": (_int, [_vp, _vp, _u64, _vp, _vp]),
     "rplhip_mse_backward": (_int, [_vp, _vp, _u64, _vp, _vp, _vp]),
     "rplhip_sgd_step": (_int, [_vp, _vp, _vp, _u64, _f32, _f32, _f32, _f32, _int, _vp]),
+    "rplhip_sigmoid": (_int, [_vp, _vp, _u64, _vp]),
+    "rplhip_tanh": (_int, [_vp, _vp, _u64, _vp]),
+    "rplhip_gelu": (_int, [_vp, _vp, _u64, _vp]),
     "rplhip_fill": (_int, [_vp, _u64, _f32, _vp]),
     # ---- rpl.h
     "tensor_create": (_PT, [_u32, C.POINTER(_u32), C.c_bool]),
@@ -189,6 +192,9 @@ PROTOTYPES = {
     "rpl_gpu_shutdown": (None, []),
     "tensor_to_gpu": (None, [_PT]),
     "tensor_from_gpu": (None, [_PT]),
+    "tensor_sigmoid_gpu": (None, [_PT, _PT]),
+    "tensor_tanh_gpu": (None, [_PT, _PT]),
+    "tensor_gelu_gpu": (None, [_PT, _PT]),
     "tensor_add_gpu": (None, [_PT, _PT, _PT]),
     "tensor_matmul_gpu": (None, [_PT, _PT, _PT]),
     "tensor_relu_gpu": (None, [_PT, _PT]),
@@ -228,6 +234,7 @@ PROTOTYPES = {
     "optimizer_sgd_create": (C.POINTER(Optimizer), [C.POINTER(_PT), _u32, _f32, _f32, _f32, _f32, C.c_bool]),
     "optimizer_sgd_step": (None, [C.POINTER(Optimizer)]),
     "rpl_last_error": (C.c_char_p, []),
+    "rpl_clear_last_error": (None, []),
     "rpl_gpu_synchronize": (None, []),
     "rpl_gpu_stream": (_vp, []),
     "rpl_tensor_device_data": (_fp, [_PT]),

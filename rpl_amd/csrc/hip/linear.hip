@@ -1,6 +1,8 @@
 // Elementwise and reduction kernels around the Linear GEMMs: bias add (+ReLU),
 // ReLU backward, gradient accumulation, the bias-gradient column reduction and
 // the MSE loss / backward.  All are HBM- or launch-bound; the GEMMs dominate.
+#include <math.h>
+
 #include "common.h"
 
 namespace {
@@ -137,6 +139,31 @@ __global__ void __launch_bounds__(kThreads) k_mse_backward(const float* __restri
     float factor = 2.0f / (float)n;
     float g0 = *g0p;
     GRID_STRIDE(i, n) { dp[i] += g0 * factor * (p[i] - t[i]); }
+}
+
+// Activations of the device seam (tensor_sigmoid_gpu / tensor_tanh_gpu /
+// tensor_gelu_gpu, src/rpl_gpu.c:437-522) with the reference's CPU formulas
+// (tensor_sigmoid src/rpl_core.c:302-304, tensor_tanh_inplace :490-491,
+// tensor_gelu_inplace :493-497) on the device's expf / tanhf / powf.  GCC
+// contracts the GELU inner sum to fma(0.044715f, x^3, x); gelu_c is
+// sqrtf(2/pi) as the reference computes it (passed in from the host).
+enum Act { kSigmoid = 0, kTanh = 1, kGelu = 2 };
+template <int ACT>
+__global__ void __launch_bounds__(kThreads) k_act(const float* __restrict__ x, float* __restrict__ y, uint64_t n,
+                                                  float gelu_c) {
+#pragma clang fp contract(off)
+    GRID_STRIDE(i, n) {
+        const float v = x[i];
+        float r;
+        if constexpr (ACT == kSigmoid) {
+            r = 1.0f / (1.0f + expf(-v));
+        } else if constexpr (ACT == kTanh) {
+            r = tanhf(v);
+        } else {
+            r = 0.5f * v * (1.0f + tanhf(gelu_c * __fmaf_rn(0.044715f, powf(v, 3.0f), v)));
+        }
+        y[i] = r;
+    }
 }
 
 // optimizer_sgd_step (src/rpl_training.c:70-114), one element per thread.
@@ -288,6 +315,33 @@ int rplhip_mse_backward(const float* pred, const float* target, uint64_t n, cons
     hipLaunchKernelGGL(k_mse_backward, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), pred,
                        target, n, g0, dpred);
     return check_launch("mse_backward");
+}
+
+static int launch_act(int act, const float* x, float* y, uint64_t n, rplhip_stream_t stream, const char* what) {
+    if (n == 0) return RPLHIP_OK;
+    if (!x || !y) return fail(RPLHIP_ERR_INVALID, "%s: NULL pointer", what);
+    RPLHIP_REQUIRE_DEVICE();
+    const float gelu_c = sqrtf((float)(2.0 / M_PI));  // host libm: correctly rounded, as the reference's
+    const dim3 g(grid_for(n)), b(kThreads);
+    if (act == kSigmoid)
+        hipLaunchKernelGGL(k_act<kSigmoid>, g, b, 0, as_stream(stream), x, y, n, gelu_c);
+    else if (act == kTanh)
+        hipLaunchKernelGGL(k_act<kTanh>, g, b, 0, as_stream(stream), x, y, n, gelu_c);
+    else
+        hipLaunchKernelGGL(k_act<kGelu>, g, b, 0, as_stream(stream), x, y, n, gelu_c);
+    return check_launch(what);
+}
+
+int rplhip_sigmoid(const float* x, float* y, uint64_t n, rplhip_stream_t stream) {
+    return launch_act(kSigmoid, x, y, n, stream, "rplhip_sigmoid");
+}
+
+int rplhip_tanh(const float* x, float* y, uint64_t n, rplhip_stream_t stream) {
+    return launch_act(kTanh, x, y, n, stream, "rplhip_tanh");
+}
+
+int rplhip_gelu(const float* x, float* y, uint64_t n, rplhip_stream_t stream) {
+    return launch_act(kGelu, x, y, n, stream, "rplhip_gelu");
 }
 
 int rplhip_sgd_step(float* param, float* grad, float* velocity, uint64_t n, float lr, float momentum,

@@ -20,6 +20,12 @@ void tensor_add_out(Tensor* out, const Tensor* a, const Tensor* b) {
         rpl__bad("tensor_add_out", "bad arguments");
         return;
     }
+    /* The reference reads a[i] for every output element and b[i % b->size]
+     * and overruns when the sizes disagree; here that is an error. */
+    if (a->size != out->size || out->size % b->size) {
+        rpl__bad("tensor_add_out", "sizes %u + %u -> %u do not broadcast", a->size, b->size, out->size);
+        return;
+    }
     if (!rpl_gpu_init()) return;
     RplStage s = {0};
     const float* da = rpl__view_data(&s, a, 1, 0);
@@ -73,15 +79,48 @@ Tensor* tensor_relu(const Tensor* t) {
     return out;
 }
 
-void tensor_relu_gpu(Tensor* out, const Tensor* in) {
+/* The device seam's elementwise ops (src/rpl_gpu.c:437-522, dispatch_unary_op):
+ * `in` moves to the device; an output that is not resident takes in's
+ * shape and becomes resident, as the reference does -- provided its host
+ * buffer holds that many elements (the reference would overrun it).  A
+ * resident output must already have in's size. */
+static void unary_gpu(Tensor* out, const Tensor* in, int (*fn)(const float*, float*, uint64_t, rplhip_stream_t),
+                      const char* what) {
+    if (!out || !in) {
+        rpl__bad(what, "NULL tensor");
+        return;
+    }
+    if (!rpl_gpu_init()) return;
     tensor_to_gpu((Tensor*)in);
-    if (!rpl__is_gpu(out) && !rpl__attach(out, 0)) return;
+    if (!rpl__is_gpu(in)) return;
+    if (!rpl__is_gpu(out)) {
+        if (out->size < in->size) {
+            rpl__bad(what, "output holds %u elements, input has %u", out->size, in->size);
+            return;
+        }
+        out->dims = in->dims;
+        memcpy(out->shape, in->shape, sizeof(in->shape));
+        out->size = in->size;
+        if (!rpl__attach(out, 0)) return;
+    } else if (out->size != in->size) {
+        rpl__bad(what, "output has %u elements, input has %u", out->size, in->size);
+        return;
+    }
     RplStage s = {0};
     const float* dx = rpl__view_data(&s, in, 1, 0);
     float* dy = rpl__view_data(&s, out, 0, 1);
-    if (!s.err) s.err = !rpl__ok(rplhip_relu(dx, dy, in->size, NULL), "tensor_relu_gpu");
+    if (!s.err) s.err = !rpl__ok(fn(dx, dy, in->size, NULL), what);
     rpl__stage_finish(&s);
 }
+
+/* src/rpl_gpu.c:475-477 */
+void tensor_relu_gpu(Tensor* out, const Tensor* in) { unary_gpu(out, in, rplhip_relu, "tensor_relu_gpu"); }
+/* src/rpl_gpu.c:479-481 (CPU formula: tensor_sigmoid, src/rpl_core.c:302-304) */
+void tensor_sigmoid_gpu(Tensor* out, const Tensor* in) { unary_gpu(out, in, rplhip_sigmoid, "tensor_sigmoid_gpu"); }
+/* src/rpl_gpu.c:515-517 (CPU formula: tensor_tanh_inplace, src/rpl_core.c:490-491) */
+void tensor_tanh_gpu(Tensor* out, const Tensor* in) { unary_gpu(out, in, rplhip_tanh, "tensor_tanh_gpu"); }
+/* src/rpl_gpu.c:519-521 (CPU formula: tensor_gelu_inplace, src/rpl_core.c:493-497) */
+void tensor_gelu_gpu(Tensor* out, const Tensor* in) { unary_gpu(out, in, rplhip_gelu, "tensor_gelu_gpu"); }
 
 /* src/rpl_core.c:449-465 */
 Tensor* tensor_mse_loss(const Tensor* pred, const Tensor* target) {

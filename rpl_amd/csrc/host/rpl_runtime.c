@@ -17,6 +17,7 @@
 static __thread char g_last_error[512];
 
 const char* rpl_last_error(void) { return g_last_error; }
+void rpl_clear_last_error(void) { g_last_error[0] = '\0'; }
 
 int rpl__ok(int st, const char* what) {
     if (st == RPLHIP_OK) return 1;

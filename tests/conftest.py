@@ -51,6 +51,15 @@ def gpu(rpl):
     return rpl
 
 
+@pytest.fixture(autouse=True)
+def _clean_last_error(request):
+    """rpl_last_error() keeps the last failure of the thread: start every
+    test that uses the library with a clean slate."""
+    if "rpl" in request.fixturenames or "gpu" in request.fixturenames:
+        request.getfixturevalue("rpl").rpl_clear_last_error()
+    yield
+
+
 def bits_equal(a, b):
     """Bit-level equality (NaN payloads and signed zeros included)."""
     a = np.ascontiguousarray(a)

@@ -68,6 +68,9 @@ def load_ref():
         "parallel_gemm_optimized": (None, [C.c_void_p, C.c_void_p, C.c_void_p, u32, u32, u32]),
         "optimizer_sgd_create": (C.POINTER(Optimizer), [C.POINTER(PT), u32, f32, f32, f32, f32, b]),
         "optimizer_sgd_step": (None, [C.POINTER(Optimizer)]),
+        "tensor_sigmoid": (PT, [PT]),
+        "tensor_tanh_inplace": (None, [PT]),
+        "tensor_gelu_inplace": (None, [PT]),
     }
     for n, (r, a) in protos.items():
         f = getattr(lib, n)
@@ -345,6 +348,21 @@ def main():
                 if mom:
                     g[f"sgd_{name}_s{step}_v{k}"] = ref.data(st.velocity[k])
         g[f"sgd_{name}_hyper"] = np.array([lr, mom, damp, wd, float(nest)], np.float32)
+
+    # ---- activations of the device seam, CPU formulas (rpl_core.c:302-304,
+    # 490-497): uniform inputs plus specials (signed zeros, subnormals, the
+    # exp overflow edges, +-inf, NaN, huge values).
+    rng = np.random.default_rng(seed(6, 0))
+    specials = np.array([0.0, -0.0, 1e-40, -1e-40, 1e-8, -1e-8, 88.7, -88.7, 88.8, -88.8, 100.0, -100.0,
+                         np.inf, -np.inf, np.nan, 3.4e38, -3.4e38, 0.5, -0.5, 3.0, -3.0], np.float32)
+    xa = np.concatenate([rng.uniform(-12, 12, 4096).astype(np.float32), specials])
+    g["act_x"] = xa
+    t = ref.tensor(xa)
+    g["act_sigmoid"] = ref.data(L.tensor_sigmoid(t))
+    for kind in ("tanh", "gelu"):
+        t = ref.tensor(xa)
+        getattr(L, f"tensor_{kind}_inplace")(t)
+        g[f"act_{kind}"] = ref.data(t)
 
     # ---- configs 0 and 1 at 512^3: hashes of the reference outputs
     n = 512

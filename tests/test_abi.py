@@ -95,3 +95,16 @@ def test_generator_pinned_and_split_independent():
     assert abs(z.mean()) < 0.01 and abs(z.std() - 1) < 0.01
     labels, one_hot = rpl_amd.fill_labels(5000, 7, 10)
     assert labels.max() == 9 and np.array_equal(one_hot.argmax(1), labels) and np.all(one_hot.sum(1) == 1)
+
+
+def test_add_out_rejects_sizes_that_do_not_broadcast(rpl):
+    # The reference overruns its buffers here; the size check comes before
+    # any device work, so it is visible without a GPU.
+    def mk(n):
+        shape = (C.c_uint32 * 1)(n)
+        return rpl.tensor_create(1, shape, False)
+    out, a, b = mk(12), mk(10), mk(4)
+    rpl.tensor_add_out(out, a, b)
+    assert b"do not broadcast" in rpl.rpl_last_error()
+    for t in (out, a, b):
+        rpl.tensor_free(t)

@@ -342,3 +342,28 @@ def test_sgd_step_closed_forms(orc):
     pw, gw = p0.copy(), np.zeros_like(p0)
     orc.sgd_step(pw, gw, None, 0.0, 0.0, 0.0, 0.25, False)
     assert bits_equal(gw, (np.float32(0.25) * p0).astype(np.float32)) and bits_equal(pw, p0)
+
+
+@pytest.mark.parametrize("kind", ["sigmoid", "tanh", "gelu"])
+def test_activations_golden(orc, golden, kind):
+    # tensor_sigmoid / tensor_tanh_inplace / tensor_gelu_inplace
+    # (rpl_core.c:302-304, 490-497) on the reference build's inputs.
+    assert bits_equal(orc.activation(kind, golden["act_x"]), golden[f"act_{kind}"])
+
+
+def test_activations_float64(orc):
+    # The mathematics in float64 (numpy's exp/tanh, an independent
+    # implementation): each float32 result within a few ulp, plus exact
+    # special values.
+    x = np.linspace(-9, 9, 20001).astype(np.float32)
+    x64 = x.astype(np.float64)
+    ref = {"sigmoid": 1 / (1 + np.exp(-x64)), "tanh": np.tanh(x64),
+           "gelu": 0.5 * x64 * (1 + np.tanh(np.sqrt(2 / np.pi) * (x64 + 0.044715 * x64 ** 3)))}
+    for kind, r in ref.items():
+        y = orc.activation(kind, x).astype(np.float64)
+        tol = 4 * np.spacing(np.abs(r).astype(np.float32)).astype(np.float64) + (2.0 ** -22) * np.abs(x64) * (
+            kind == "gelu")
+        assert np.all(np.abs(y - r) <= tol), kind
+    z = np.float32([0.0])
+    assert orc.activation("sigmoid", z)[0] == 0.5 and orc.activation("tanh", z)[0] == 0.0
+    assert orc.activation("gelu", z)[0] == 0.0
