@@ -1257,15 +1257,17 @@ __global__ void __launch_bounds__(256) k_rowsum_i8(const int8_t* __restrict__ X,
 
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
-// Tile configuration: the 256 x 256 tile when it still gives every CU at
-// least two tiles, else 128 x 128.  RPLHIP_I8_TILE=small|big overrides (for
-// tuning sweeps only).
-bool use_big_tile(uint32_t M, uint32_t N) {
+// Tile configuration: 256 x 256 tiles on the direct-to-LDS kernel from 3/4
+// of a tile per CU (config 3, 2048 x 11008 x 4096: 344 tiles on 256 CUs,
+// 123 us against 155 us with 128 x 128 tiles; at half a tile per CU the
+// small tiles win), on the register-staged kernel from two tiles per CU;
+// else 128 x 128.  RPLHIP_I8_TILE=small|big overrides (tuning sweeps only).
+bool use_big_tile(uint32_t M, uint32_t N, bool dma) {
     static const char* env = getenv("RPLHIP_I8_TILE");
     if (env && env[0] == 's') return false;
     if (env && env[0] == 'b') return true;
-    uint64_t tiles = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
-    return tiles >= 2ull * rplhip::cu_count();
+    const uint64_t tiles = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
+    return dma ? 4 * tiles >= 3ull * rplhip::cu_count() : tiles >= 2ull * rplhip::cu_count();
 }
 
 // The direct-to-LDS kernel serves the big tile unless RPLHIP_I8_DMA=0 (for
@@ -1348,8 +1350,10 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
     }
     // Odd shapes (byte-wise loads) always take the small tile: the big one
     // has no registers to spare for them.
-    if (al && use_big_tile(M, N)) {
-        if (K % dma::BK == 0 && (uint64_t)M * lda < (1ull << 31) && (uint64_t)N * ldb < (1ull << 31) && use_dma()) {
+    const bool dma_ok =
+        al && K % dma::BK == 0 && (uint64_t)M * lda < (1ull << 31) && (uint64_t)N * ldb < (1ull << 31) && use_dma();
+    if (al && use_big_tile(M, N, dma_ok)) {
+        if (dma_ok) {
             const uint64_t tiles = (uint64_t)((M + dma::BM - 1) / dma::BM) * ((N + dma::BN - 1) / dma::BN);
             if (RPL_I8_BIG_KERNEL == 1)
                 hipLaunchKernelGGL((k_gemm_i8_nt_pp<EPI>), dim3((uint32_t)tiles), dim3(pp::kThreads), 0, s, A, lda,
