@@ -392,7 +392,8 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt(const int8_t* __restrict_
     });
 }
 
-// Fused epilogue straight from MFMA accumulators: FM x FN blocks of 32x32;
+// Fused epilogue straight from MFMA accumulators: FM x FN blocks of 32x32
+// (acc may be wider, FNA >= FN columns, the rest unused);
 // result register r of lane l in block (i, j) is row mb + i*32 + 8*(r/4) +
 // r%4 and column nb + j*32, where mb = tile row + 4*(l/32) and nb = tile
 // column + l%32.  Fully unrolled (the accumulators are only ever indexed by
@@ -400,8 +401,8 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt(const int8_t* __restrict_
 // column, those that depend on the row once per row.  Each store
 // instruction writes two 128-byte row segments.  This is the bounds-checked
 // form for edge tiles; epilogue_tile_full serves interior ones.
-template <int EPI, int FM, int FN>
-__device__ __forceinline__ void epilogue_tile(const EpiParams& p, const v16i (&acc)[FM][FN], uint32_t mb,
+template <int EPI, int FM, int FN, int FNA = FN>
+__device__ __forceinline__ void epilogue_tile(const EpiParams& p, const v16i (&acc)[FM][FNA], uint32_t mb,
                                               uint32_t nb, uint32_t M, uint32_t N) {
     int32_t cadd[FN];  // kRaw: bias[n]
     float cmul[FN];    // kDequant: sw[n]
@@ -444,8 +445,8 @@ constexpr uint32_t kFullEpiMaxLdc = 1u << 21;
 // column l%32) is one VGPR offset, the row of result register r (a
 // constant times ldc) goes in the scalar offset and the 32-column block in
 // the instruction's immediate offset.
-template <int EPI, int FM, int FN>
-__device__ __forceinline__ void epilogue_tile_full(const EpiParams& p, const v16i (&acc)[FM][FN], uint32_t wm0,
+template <int EPI, int FM, int FN, int FNA = FN>
+__device__ __forceinline__ void epilogue_tile_full(const EpiParams& p, const v16i (&acc)[FM][FNA], uint32_t wm0,
                                                    uint32_t wn0, uint32_t lane) {
     const uint32_t ldc4 = p.ldc * 4;
     const void* out = EPI == kDequant ? (const void*)p.out_f32 : (const void*)p.out_i32;
@@ -501,13 +502,25 @@ __device__ __forceinline__ void epilogue_tile_full(const EpiParams& p, const v16
 #endif
 
 namespace dma {
-constexpr int BM = 256, BN = 256, BK = 64, S = RPL_I8_STAGES, kThreads = 256;
+constexpr int BM = 256, BK = 64, S = RPL_I8_STAGES, kThreads = 256;
 constexpr int kSlot = RPL_I8_DMA_SLOT;
-static_assert(S >= 3 && S * (BM + BN) * BK <= 160 * 1024, "LDS ring must fit 160 KB");
-constexpr int kTileBytes = BM * BK;          // one operand of one stage: 16 KB
-constexpr int kStageBytes = (BM + BN) * BK;  // 32 KB
-constexpr int kLoads = 4;                    // 1 KB loads per wave per operand per tile
-constexpr int kVmPerTile = 2 * kLoads;       // load instructions per wave per tile
+// B-tile height BN = 256 (the big tile) or 128 (grids with too few 256 x
+// 256 tiles to fill the chip): 4 waves (2 x 2), wave tile 128 x BN/2.
+template <int BN>
+struct Geo {
+    static_assert(BN == 256 || BN == 128, "B tile of 256 or 128 rows");
+    static_assert(S >= 3 && S * (BM + BN) * BK <= 160 * 1024, "LDS ring must fit 160 KB");
+    static constexpr int FN = BN / 64;                    // 32-wide MFMA blocks per wave (N side)
+    static constexpr int kTileBytesA = BM * BK;           // A part of one stage: 16 KB
+    static constexpr int kStageBytes = (BM + BN) * BK;
+    static constexpr int kLoadsA = BM / 64, kLoadsB = BN / 64;  // 1 KB copies per wave per tile
+    static constexpr int kVmPerTile = kLoadsA + kLoadsB;  // copy instructions per wave per tile
+};
+// Fragments of one 32-k step: 4 A blocks, FN B blocks.
+template <int FN>
+struct Frags {
+    v4i a[4], b[FN];
+};
 }  // namespace dma
 
 // Same tiles, MFMA and fused epilogues as k_gemm_i8_nt<CfgBig>, with the
@@ -531,11 +544,17 @@ constexpr int kVmPerTile = 2 * kLoads;       // load instructions per wave per t
 //
 // Requires K % 64 == 0, 16-byte aligned operands and leading dimensions,
 // and operands below 2 GiB (32-bit buffer offsets).
-template <int EPI>
+template <int EPI, int BN>
 __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restrict__ A, uint32_t lda,
                                                            const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
                                                            uint32_t N, uint32_t K, EpiParams p) {
-    using namespace dma;
+    using dma::BK;
+    using dma::BM;
+    using dma::kSlot;
+    using dma::S;
+    using G = dma::Geo<BN>;
+    constexpr int FN = G::FN, kLoadsA = G::kLoadsA, kLoadsB = G::kLoadsB, kVmPerTile = G::kVmPerTile;
+    constexpr int kTileBytesA = G::kTileBytesA, kStageBytes = G::kStageBytes;
     __shared__ __attribute__((aligned(1024))) int8_t smem[S * kStageBytes];
 
     const uint32_t lane = threadIdx.x % 64;
@@ -549,29 +568,35 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
     const __amdgpu_buffer_rsrc_t rsrc_a = uniform_rsrc(A + (uint64_t)m0 * lda, rows_a * lda);
     const __amdgpu_buffer_rsrc_t rsrc_b = uniform_rsrc(B + (uint64_t)n0 * ldb, rows_b * ldb);
 
-    // Source offsets of this lane's four A and four B copies (k added as the
-    // scalar offset).
-    uint32_t voff_a[kLoads], voff_b[kLoads];
+    // Source offsets of this lane's A and B copies (k added as the scalar
+    // offset): wave w copies rows w*BM/4 .. and w*BN/4 .. of the tiles.
+    // (Array bounds here must not depend on BN: the host pass of hipcc then
+    // drops the kernel's launch stub without a diagnostic.  Sized for the
+    // largest tile; loops run to kLoadsA / kLoadsB / FN.)
+    uint32_t voff_a[4], voff_b[4];
 #pragma unroll
-    for (int i = 0; i < kLoads; i++) {
-        const uint32_t r = wave * 64 + i * 16 + lane / 4;
-        const uint32_t c = ((lane % 4) ^ swz(r)) * 16;
-        voff_a[i] = (r < rows_a ? r : rows_a - 1) * lda + c;
-        voff_b[i] = (r < rows_b ? r : rows_b - 1) * ldb + c;
+    for (int i = 0; i < kLoadsA; i++) {
+        const uint32_t r = wave * (BM / 4) + i * 16 + lane / 4;
+        voff_a[i] = (r < rows_a ? r : rows_a - 1) * lda + ((lane % 4) ^ swz(r)) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < kLoadsB; i++) {
+        const uint32_t r = wave * (BN / 4) + i * 16 + lane / 4;
+        voff_b[i] = (r < rows_b ? r : rows_b - 1) * ldb + ((lane % 4) ^ swz(r)) * 16;
     }
     auto issue_a = [&](uint32_t kt, uint32_t stage) {
         int8_t* st = smem + stage * kStageBytes;
 #pragma unroll
-        for (int i = 0; i < kLoads; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr)(st + (wave * 64 + i * 16) * BK), 16,
+        for (int i = 0; i < kLoadsA; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr)(st + (wave * (BM / 4) + i * 16) * BK), 16,
                                                      voff_a[i], kt * BK, 0, 0);
     };
     auto issue_b = [&](uint32_t kt, uint32_t stage) {
         int8_t* st = smem + stage * kStageBytes;
 #pragma unroll
-        for (int i = 0; i < kLoads; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr)(st + kTileBytes + (wave * 64 + i * 16) * BK),
-                                                     16, voff_b[i], kt * BK, 0, 0);
+        for (int i = 0; i < kLoadsB; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsrc_b, (lds_ptr)(st + kTileBytesA + (wave * (BN / 4) + i * 16) * BK), 16, voff_b[i], kt * BK, 0, 0);
     };
     auto issue = [&](uint32_t kt, uint32_t stage) {
         issue_a(kt, stage);
@@ -593,26 +618,52 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
     uint32_t foff[2];
 #pragma unroll
     for (int kk = 0; kk < 2; kk++) foff[kk] = fr * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
-    const uint32_t a_base = wm * 128 * BK, b_base = kTileBytes + wn * 128 * BK;
-    typedef Frags<CfgBig> F;
+    const uint32_t a_base = wm * 128 * BK, b_base = kTileBytesA + wn * (BN / 2) * BK;
+    using F = dma::Frags<FN>;
     auto fload = [&](uint32_t stage, int kk, F& f) {
         const int8_t* st = smem + stage * kStageBytes + foff[kk];
 #pragma unroll
         for (int i = 0; i < 4; i++) f.a[i] = *reinterpret_cast<const v4i*>(st + a_base + i * 32 * BK);
 #pragma unroll
-        for (int j = 0; j < 4; j++) f.b[j] = *reinterpret_cast<const v4i*>(st + b_base + j * 32 * BK);
+        for (int j = 0; j < FN; j++) f.b[j] = *reinterpret_cast<const v4i*>(st + b_base + j * 32 * BK);
     };
     v16i acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = (v16i){};
+        for (int j = 0; j < FN; j++) acc[i][j] = (v16i){};
     auto mma = [&](const F& f) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
+            for (int j = 0; j < FN; j++)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+    };
+    // Pin one half's order: fragment reads one per MFMA early, then the
+    // copies of that half (BN = 128 has 8 MFMAs for 6 reads and up to 4
+    // copies: the last two MFMAs take two copies each).
+    auto pin = [&](auto copies_c) {
+        constexpr int copies = decltype(copies_c)::value;
+        if constexpr (FN == 4) {
+            static_for<8>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            });
+            static_for<copies>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // HBM -> LDS copy
+            });
+        } else {
+            constexpr int reads = 4 + FN, rest = 4 * FN - reads;
+            static_for<reads>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            });
+            static_for<rest>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, (copies + rest - 1) / rest, 0);
+            });
+        }
     };
 
     const uint32_t nk = K / BK;
@@ -636,8 +687,8 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
     // tile copies between the later MFMAs, so the MFMA pipe never waits on
     // an LDS read issued just before it (left alone, the scheduler sinks
     // every read to just before its first use and reuses its registers).
-    constexpr int kCopiesA = kSlot == 0 ? 2 * kLoads : kSlot == 2 ? kLoads : 0;
-    constexpr int kCopiesB = 2 * kLoads - kCopiesA;
+    constexpr int kCopiesA = kSlot == 0 ? kVmPerTile : kSlot == 2 ? kLoadsA : 0;
+    constexpr int kCopiesB = kVmPerTile - kCopiesA;
     // Copies issued after tile kt+1's at the barrier of iteration kt.
     constexpr int kLaterSteady = (S - 3) * kVmPerTile + kCopiesA;
     uint32_t kt = 0;
@@ -649,14 +700,7 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
             if constexpr (kSlot == 0) issue_b(kt + u + S - 1, (u + S - 1) % S);
             fload(u, 1, f1);
             mma(f0);
-            static_for<8>([&](auto) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-            });
-            static_for<kCopiesA>([&](auto) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // HBM -> LDS copy
-            });
+            pin(std::integral_constant<int, kCopiesA>{});
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLaterSteady, 0));
             __builtin_amdgcn_s_barrier();
@@ -665,14 +709,7 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
             if constexpr (kSlot != 0) issue_b(kt + u + S - 1, (u + S - 1) % S);
             fload((u + 1) % S, 0, f0);
             mma(f1);
-            static_for<8>([&](auto) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-            });
-            static_for<kCopiesB>([&](auto) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // HBM -> LDS copy
-            });
+            pin(std::integral_constant<int, kCopiesB>{});
             __builtin_amdgcn_sched_barrier(0);
         });
     }
@@ -689,9 +726,10 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
     }
 
     if (m0 + BM <= M && n0 + BN <= N && p.ldc <= kFullEpiMaxLdc)
-        epilogue_tile_full<EPI, 4, 4>(p, acc, m0 + wm * 128, n0 + wn * 128, lane);
+        epilogue_tile_full<EPI, 4, FN, 4>(p, acc, m0 + wm * 128, n0 + wn * (BN / 2), lane);
     else
-        epilogue_tile<EPI, 4, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * 128 + lane % 32, M, N);
+        epilogue_tile<EPI, 4, FN, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * (BN / 2) + lane % 32, M,
+                                     N);
 }
 
 // --------------------------- NT core GEMM, 8-wave ping-pong (2 waves/SIMD)
@@ -1270,6 +1308,12 @@ bool use_big_tile(uint32_t M, uint32_t N, bool dma) {
     return dma ? 4 * tiles >= 3ull * rplhip::cu_count() : tiles >= 2ull * rplhip::cu_count();
 }
 
+// 256 x 128 tiles unless RPLHIP_I8_TILE=small (for A/B timing only).
+bool use_half_tile() {
+    static const char* env = getenv("RPLHIP_I8_TILE");
+    return !(env && env[0] == 's');
+}
+
 // The direct-to-LDS kernel serves the big tile unless RPLHIP_I8_DMA=0 (for
 // A/B timing only).
 bool use_dma() {
@@ -1352,18 +1396,27 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
     // has no registers to spare for them.
     const bool dma_ok =
         al && K % dma::BK == 0 && (uint64_t)M * lda < (1ull << 31) && (uint64_t)N * ldb < (1ull << 31) && use_dma();
+    const uint64_t mt = (M + dma::BM - 1) / dma::BM;
     if (al && use_big_tile(M, N, dma_ok)) {
         if (dma_ok) {
-            const uint64_t tiles = (uint64_t)((M + dma::BM - 1) / dma::BM) * ((N + dma::BN - 1) / dma::BN);
+            const uint64_t tiles = mt * ((N + 255) / 256);
             if (RPL_I8_BIG_KERNEL == 1)
                 hipLaunchKernelGGL((k_gemm_i8_nt_pp<EPI>), dim3((uint32_t)tiles), dim3(pp::kThreads), 0, s, A, lda,
                                    B, ldb, M, N, K, p);
             else
-                hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI>), dim3((uint32_t)tiles), dim3(dma::kThreads), 0, s, A, lda,
-                                   B, ldb, M, N, K, p);
+                hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256>), dim3((uint32_t)tiles), dim3(dma::kThreads), 0, s, A,
+                                   lda, B, ldb, M, N, K, p);
             return rplhip::check_launch("int8 GEMM");
         }
         return launch_nt<CfgBig, EPI>(A, lda, B, ldb, M, N, K, p, al, s);
+    }
+    // Too few 256 x 256 tiles: 256 x 128 ones on the same kernel when they
+    // give at least 3/4 of a tile per CU (config 3, 2048 x 4096 x 4096: 256).
+    const uint64_t tiles_half = mt * ((N + 127) / 128);
+    if (dma_ok && use_half_tile() && 4 * tiles_half >= 3ull * rplhip::cu_count()) {
+        hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 128>), dim3((uint32_t)tiles_half), dim3(dma::kThreads), 0, s, A, lda,
+                           B, ldb, M, N, K, p);
+        return rplhip::check_launch("int8 GEMM");
     }
     return launch_nt<CfgSmall, EPI>(A, lda, B, ldb, M, N, K, p, al, s);
 }

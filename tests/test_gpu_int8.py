@@ -226,7 +226,9 @@ def _requant_f32(acc, sa, sb, sc):
 # 3 and 5 tiles.  The first two shapes have ragged edges in M and N, so both
 # the bounds-checked epilogue (edge tiles) and the unchecked buffer-store
 # epilogue (interior tiles) run; gemm_int8 transposes B [K,N] first.
-BIG = [(5890, 5900, 832), (5890, 5888, 832), (6144, 6144, 448)]
+# (1800, 3000, 448) has too few 256 x 256 tiles and takes 256 x 128 ones
+# (192 of them), with ragged M and N edges.
+BIG = [(5890, 5900, 832), (5890, 5888, 832), (6144, 6144, 448), (1800, 3000, 448)]
 
 
 @pytest.mark.parametrize("M,N,K", BIG)
