@@ -991,7 +991,11 @@ __global__ void __launch_bounds__(64 * WAVES) k_skinny(const int8_t* __restrict_
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t n0 = blockIdx.x * 16 * PANELS;
-    const uint32_t kbeg = wave * kpw < K ? wave * kpw : K, kend = kbeg + kpw < K ? kbeg + kpw : K;
+    // Wave w of block b takes K slice (w + b) % WAVES: neighbouring blocks
+    // read different parts of A at any moment (the int32 sum over the waves
+    // is exact in any order).
+    const uint32_t slice = (wave + blockIdx.x) % WAVES;
+    const uint32_t kbeg = slice * kpw < K ? slice * kpw : K, kend = kbeg + kpw < K ? kbeg + kpw : K;
     int8_t* const lds = lds_all + wave * kBufs * kStageBytes;
     auto wbuf = [&](int q) { return lds + q * kStageBytes; };
     int8_t* const xbuf = lds + PANELS * kStageBytes;
