@@ -28,6 +28,8 @@
 //   kRequant     : out = x86((int32)roundf(((float)acc*sa)*sb/sc)), optional
 //                  zero-point correction                      (gemm_int8)
 //   kRequantPow2 : kRequant with sc = +-2^k, where x/sc == x*(1/sc) exactly
+//   kRequantUnit : kRequant with sc = 1 and |acc*sa*sb| < 2^30 proven on the
+//                  host (no NaN, no overflow): no divide and no range test
 //   kDequant     : y = ((float)acc * sx[m|0]) * sw[n|0]       (fused fp32 output)
 #include <math.h>
 #include <stdlib.h>
@@ -45,7 +47,7 @@ using rplhip::tile_of;
 using rplhip::uniform_rsrc;
 using rplhip::waitcnt_imm;
 
-enum Epi { kRaw = 0, kRequant = 1, kDequant = 2, kRequantPow2 = 3 };
+enum Epi { kRaw = 0, kRequant = 1, kDequant = 2, kRequantPow2 = 3, kRequantUnit = 4 };
 
 struct EpiParams {
     // kRaw
@@ -86,6 +88,10 @@ __device__ __forceinline__ uint32_t epi_bits(const EpiParams& p, int32_t acc, ui
         return (uint32_t)x86_round_cvt((float)v * p.sa * p.sb / p.sc);
     } else if constexpr (EPI == kRequantPow2) {
         return (uint32_t)x86_round_cvt((float)acc * p.sa * p.sb * p.inv_sc);
+    } else if constexpr (EPI == kRequantUnit) {
+        // x86_round_cvt without its range test (the sum is within +-2^30).
+        const float y = (float)acc * p.sa * p.sb;
+        return (uint32_t)(int32_t)(y + __builtin_copysignf(0.49999997f, y));
     } else {
         return __float_as_uint((float)acc * rmul * cmul);
     }
@@ -1438,6 +1444,15 @@ bool exact_reciprocal(float sc, float* inv) {
     return true;
 }
 
+// True when every requantized value ((float)acc * sa) * sb of a K-long int8
+// dot product (|acc| <= K * 128 * 128) is finite and below 2^30 in
+// magnitude, so the x86 range test of the conversion can never fire.
+bool requant_in_range(uint32_t K, float sa, float sb) {
+    if (!isfinite(sa) || !isfinite(sb)) return false;
+    const double bound = (double)K * 16384.0 * fabs((double)sa) * fabs((double)sb) * (1.0 + 1e-6);
+    return bound < 1073741824.0;
+}
+
 int transpose_b(const int8_t* B, uint32_t K, uint32_t N, int8_t* Bt, hipStream_t s) {
     const uint64_t tr_tiles = (uint64_t)(N / kTrTile) * (K / kTrTile);
     if (K % kTrTile == 0 && N % kTrTile == 0 && aligned16(B) && aligned16(Bt) && tr_tiles <= 0x7fffffffull) {
@@ -1520,7 +1535,9 @@ int rplhip_gemm_int8(const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, u
         st = check_launch("int8 column sums");
     }
     if (!st) {
-        if (za == 0 && zb == 0 && exact_reciprocal(sc, &p.inv_sc))
+        if (za == 0 && zb == 0 && sc == 1.0f && requant_in_range(K, sa, sb))
+            st = run_nt<kRequantUnit>(A, K, Bt, K, M, N, K, p, s);
+        else if (za == 0 && zb == 0 && exact_reciprocal(sc, &p.inv_sc))
             st = run_nt<kRequantPow2>(A, K, Bt, K, M, N, K, p, s);
         else
             st = run_nt<kRequant>(A, K, Bt, K, M, N, K, p, s);

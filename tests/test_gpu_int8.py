@@ -251,9 +251,11 @@ def test_big_tile_int8_paths(gpu, orc, M, N, K):
     assert np.array_equal(a64.sum(0), Bt.astype(np.int64) @ A.astype(np.int64).sum(0))
     # gemm_int8 requant: power-of-two sc (exact-reciprocal epilogue) and a
     # generic sc; exact .5 ties (acc / 2, acc / 2 via 1/sc), overflow, and
-    # sc = 0 / sa = inf (inf and NaN quantize to INT32_MIN).
+    # sc = 0 / sa = inf (inf and NaN quantize to INT32_MIN); sc = 1 with a
+    # provably small range (no range test) and with one that overflows.
     for sa, sb, sc in ((0.013, 0.7, 0.25), (1.5, -3.0, -4.0), (2.0 ** 20, 2.0 ** 20, 2.0 ** -100), (0.013, 0.7, 0.3),
-                       (0.5, 1.0, 1.0), (1.0, 1.0, 2.0), (1.0, 1.0, 3.0), (0.013, 0.7, 0.0), (np.inf, 1.0, 1.0)):
+                       (0.5, 1.0, 1.0), (1.0, 1.0, 2.0), (1.0, 1.0, 3.0), (0.013, 0.7, 0.0), (np.inf, 1.0, 1.0),
+                       (0.013, 0.7, 1.0), (2.0 ** 20, 2.0 ** 20, 1.0)):
         out = empty((M, N), np.int32)
         say("big-tile gemm_int8", M, N, K, sa, sb, sc)
         rpl_amd.check(lib.rplhip_gemm_int8(dA.ptr, dB.ptr, out.ptr, M, N, K, sa, sb, sc, 0, 0, None))
