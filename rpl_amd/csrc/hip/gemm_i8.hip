@@ -1381,9 +1381,13 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
         kpw = (kpw + 63) / 64 * 64;
         const bool two = waves == 4 && M > RPL_SK_ONE_PANEL_MAX_M;
         const dim3 grid(two ? (N + 31) / 32 : (N + 15) / 16);
-        if (waves == 4 && two)
-            hipLaunchKernelGGL((k_skinny<EPI, 4, 2>), grid, dim3(256), 0, s, A, lda, B, ldb, M, N, K, kpw, p);
-        else if (waves == 4)
+        if constexpr (RPL_SK_ONE_PANEL_MAX_M < 16) {  // two panels are only reachable below M = 16
+            if (two) {
+                hipLaunchKernelGGL((k_skinny<EPI, 4, 2>), grid, dim3(256), 0, s, A, lda, B, ldb, M, N, K, kpw, p);
+                return rplhip::check_launch("skinny int8 GEMM");
+            }
+        }
+        if (waves == 4)
             hipLaunchKernelGGL((k_skinny<EPI, 4, 1>), grid, dim3(256), 0, s, A, lda, B, ldb, M, N, K, kpw, p);
         else
             hipLaunchKernelGGL((k_skinny<EPI, 8, 1>), grid, dim3(512), 0, s, A, lda, B, ldb, M, N, K, kpw, p);
@@ -1410,7 +1414,7 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
     if (al && use_big_tile(M, N, dma_ok)) {
         if (dma_ok) {
             const uint64_t tiles = mt * ((N + 255) / 256);
-            if (RPL_I8_BIG_KERNEL == 1)
+            if constexpr (RPL_I8_BIG_KERNEL == 1)
                 hipLaunchKernelGGL((k_gemm_i8_nt_pp<EPI>), dim3((uint32_t)tiles), dim3(pp::kThreads), 0, s, A, lda,
                                    B, ldb, M, N, K, p);
             else
