@@ -164,6 +164,12 @@ Linear* linear_create(uint32_t in_features, uint32_t out_features);
 Tensor* linear_forward(Linear* layer, const Tensor* input);
 void linear_free(Linear* layer);
 
+/* ---- attention (src/rpl_attention.c:16-111; exported there, not declared
+ * in the reference header): Q [B,Sq,dk], K [B,Sk,dk], V [B,Sk,dv], mask
+ * with B*Sq*Sk elements or NULL; dropout is a no-op as in the reference. ---- */
+Tensor* scaled_dot_product_attention(const Tensor* Q, const Tensor* K, const Tensor* V, const Tensor* mask,
+                                     float dropout_p, bool training);
+
 /* ---- SGD optimizer step on the device (include/rpl.h:306-316,
  * src/rpl_training.c:20-114).  Optimizer is opaque; its layout is the
  * reference's, so optimizers made by either library interoperate with the

@@ -190,6 +190,13 @@ int rplhip_mse_backward(const float* pred, const float* target, uint64_t n, cons
 int rplhip_sigmoid(const float* x, float* y, uint64_t n, rplhip_stream_t stream);
 int rplhip_tanh(const float* x, float* y, uint64_t n, rplhip_stream_t stream);
 int rplhip_gelu(const float* x, float* y, uint64_t n, rplhip_stream_t stream);
+/* scaled_dot_product_attention (src/rpl_attention.c:16-111), DEVICE pointers:
+ * Q [B,Sq,dk], K [B,Sk,dk], V [B,Sk,dv], mask [B,Sq,Sk] or NULL (entries
+ * == 0 become -1e9 before the softmax), out [B,Sq,dv].  scores =
+ * (Q K^T) * (1/sqrtf(dk)) on the FP32 GEMM, row softmax, out = P V.  Uses a
+ * B*Sq*Sk-float workspace. */
+int rplhip_attention(const float* Q, const float* K, const float* V, const float* mask, float* out,
+                     uint32_t B, uint32_t Sq, uint32_t Sk, uint32_t dk, uint32_t dv, rplhip_stream_t stream);
 /* optimizer_sgd_step (src/rpl_training.c:70-114) on one parameter tensor of
  * n floats, all DEVICE pointers: weight decay and Nesterov update grad in
  * place as the reference does; velocity (the momentum buffer) may be NULL

@@ -44,6 +44,7 @@ PROTOTYPES = {
     "orc_sigmoid": (None, [_vp, _vp, _u32]),
     "orc_tanh": (None, [_vp, _vp, _u32]),
     "orc_gelu": (None, [_vp, _vp, _u32]),
+    "orc_sdpa": (None, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32]),
 }
 
 
@@ -212,6 +213,16 @@ class Oracle:
         y = np.empty_like(x)
         getattr(self.lib, f"orc_{kind}")(_p(x), _p(y), x.size)
         return y
+
+    def sdpa(self, Q, K, V, mask=None):
+        """scaled_dot_product_attention: Q [B,Sq,dk], K [B,Sk,dk], V [B,Sk,dv]."""
+        Q, K, V = (np.ascontiguousarray(a, np.float32) for a in (Q, K, V))
+        B, Sq, dk = Q.shape
+        Sk, dv = K.shape[1], V.shape[2]
+        m = None if mask is None else np.ascontiguousarray(mask, np.float32)
+        out = np.empty((B, Sq, dv), np.float32)
+        self.lib.orc_sdpa(_p(Q), _p(K), _p(V), None if m is None else _p(m), _p(out), B, Sq, Sk, dk, dv)
+        return out
 
     def mlp_step(self, X, Y, W1, b1, W2, b2):
         X, Y, W1, b1, W2, b2 = (np.ascontiguousarray(v, np.float32) for v in (X, Y, W1, b1, W2, b2))

@@ -381,3 +381,55 @@ void orc_gelu(const float* x, float* y, uint32_t n) {
         y[i] = 0.5f * v * (1.0f + tanhf(sqrtf(2.0f / M_PI) * (v + 0.044715f * powf(v, 3))));
     }
 }
+
+/* scaled_dot_product_attention (rpl_attention.c:16-111) on raw arrays:
+ * Q [B,Sq,dk], K [B,Sk,dk], V [B,Sk,dv], mask [B,Sq,Sk] or NULL (0 ->
+ * -1e9 before the softmax), out [B,Sq,dv].  Dropout is the reference's
+ * no-op stub (rpl_core.c:533), so it does not appear. */
+void orc_sdpa(const float* Q, const float* K, const float* V, const float* mask, float* out, uint32_t B,
+              uint32_t Sq, uint32_t Sk, uint32_t dk, uint32_t dv) {
+    float* scores = (float*)malloc((size_t)B * Sq * Sk * sizeof(float));
+    if (!scores) return;
+    float scale = 1.0f / sqrtf((float)dk);
+#pragma omp parallel for collapse(2)
+    for (uint32_t b = 0; b < B; b++) {
+        for (uint32_t i = 0; i < Sq; i++) {
+            for (uint32_t j = 0; j < Sk; j++) {
+                float sum = 0.0f;
+                for (uint32_t k = 0; k < dk; k++) sum += Q[b * Sq * dk + i * dk + k] * K[b * Sk * dk + j * dk + k];
+                scores[b * Sq * Sk + i * Sk + j] = sum * scale;
+            }
+        }
+    }
+    if (mask) {
+#pragma omp parallel for
+        for (uint32_t i = 0; i < B * Sq * Sk; i++)
+            if (mask[i] == 0.0f) scores[i] = -1e9f;
+    }
+#pragma omp parallel for collapse(2)
+    for (uint32_t b = 0; b < B; b++) {
+        for (uint32_t i = 0; i < Sq; i++) {
+            float* row = &scores[b * Sq * Sk + i * Sk];
+            float max_val = -FLT_MAX;
+            for (uint32_t j = 0; j < Sk; j++)
+                if (row[j] > max_val) max_val = row[j];
+            float sum_exp = 0.0f;
+            for (uint32_t j = 0; j < Sk; j++) {
+                row[j] = expf(row[j] - max_val);
+                sum_exp += row[j];
+            }
+            for (uint32_t j = 0; j < Sk; j++) row[j] /= sum_exp;
+        }
+    }
+#pragma omp parallel for collapse(2)
+    for (uint32_t b = 0; b < B; b++) {
+        for (uint32_t i = 0; i < Sq; i++) {
+            for (uint32_t k = 0; k < dv; k++) {
+                float sum = 0.0f;
+                for (uint32_t j = 0; j < Sk; j++) sum += scores[b * Sq * Sk + i * Sk + j] * V[b * Sk * dv + j * dv + k];
+                out[b * Sq * dv + i * dv + k] = sum;
+            }
+        }
+    }
+    free(scores);
+}

@@ -126,6 +126,10 @@ void orc_sigmoid(const float* x, float* y, uint32_t n);
 void orc_tanh(const float* x, float* y, uint32_t n);
 void orc_gelu(const float* x, float* y, uint32_t n);
 
+/* rpl_attention.c:16-111 */
+void orc_sdpa(const float* Q, const float* K, const float* V, const float* mask, float* out, uint32_t B,
+              uint32_t Sq, uint32_t Sk, uint32_t dk, uint32_t dv);
+
 #ifdef __cplusplus
 }
 #endif

@@ -181,6 +181,7 @@ PROTOTYPES = {
     "rplhip_sigmoid": (_int, [_vp, _vp, _u64, _vp]),
     "rplhip_tanh": (_int, [_vp, _vp, _u64, _vp]),
     "rplhip_gelu": (_int, [_vp, _vp, _u64, _vp]),
+    "rplhip_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
     "rplhip_fill": (_int, [_vp, _u64, _f32, _vp]),
     # ---- rpl.h
     "tensor_create": (_PT, [_u32, C.POINTER(_u32), C.c_bool]),
@@ -233,6 +234,7 @@ PROTOTYPES = {
     "linear_free": (None, [C.POINTER(Linear)]),
     "optimizer_sgd_create": (C.POINTER(Optimizer), [C.POINTER(_PT), _u32, _f32, _f32, _f32, _f32, C.c_bool]),
     "optimizer_sgd_step": (None, [C.POINTER(Optimizer)]),
+    "scaled_dot_product_attention": (_PT, [_PT, _PT, _PT, _PT, _f32, C.c_bool]),
     "rpl_last_error": (C.c_char_p, []),
     "rpl_clear_last_error": (None, []),
     "rpl_gpu_synchronize": (None, []),

@@ -71,6 +71,7 @@ def load_ref():
         "tensor_sigmoid": (PT, [PT]),
         "tensor_tanh_inplace": (None, [PT]),
         "tensor_gelu_inplace": (None, [PT]),
+        "scaled_dot_product_attention": (PT, [PT, PT, PT, PT, f32, b]),
     }
     for n, (r, a) in protos.items():
         f = getattr(lib, n)
@@ -363,6 +364,21 @@ def main():
         t = ref.tensor(xa)
         getattr(L, f"tensor_{kind}_inplace")(t)
         g[f"act_{kind}"] = ref.data(t)
+
+    # ---- scaled_dot_product_attention (rpl_attention.c:16-111), with and
+    # without a mask (a 0/1 pattern plus one fully masked row).
+    rng = np.random.default_rng(seed(7, 0))
+    for name, (B, Sq, Sk, dk, dv) in {"small": (2, 5, 7, 8, 6), "mid": (3, 33, 65, 64, 32)}.items():
+        Q = rng.standard_normal((B, Sq, dk)).astype(np.float32)
+        Kt = rng.standard_normal((B, Sk, dk)).astype(np.float32)
+        V = rng.standard_normal((B, Sk, dv)).astype(np.float32)
+        mask = (rng.random((B, Sq, Sk)) < 0.7).astype(np.float32)
+        mask[0, Sq - 1, :] = 0.0
+        g.update({f"att_{name}_Q": Q, f"att_{name}_K": Kt, f"att_{name}_V": V, f"att_{name}_mask": mask})
+        for masked in (False, True):
+            o = L.scaled_dot_product_attention(ref.tensor(Q), ref.tensor(Kt), ref.tensor(V),
+                                               ref.tensor(mask) if masked else None, 0.0, False)
+            g[f"att_{name}_out{'_m' if masked else ''}"] = ref.data(o).reshape(B, Sq, dv)
 
     # ---- configs 0 and 1 at 512^3: hashes of the reference outputs
     n = 512

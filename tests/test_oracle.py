@@ -367,3 +367,35 @@ def test_activations_float64(orc):
     z = np.float32([0.0])
     assert orc.activation("sigmoid", z)[0] == 0.5 and orc.activation("tanh", z)[0] == 0.0
     assert orc.activation("gelu", z)[0] == 0.0
+
+
+@pytest.mark.parametrize("name", ["small", "mid"])
+@pytest.mark.parametrize("masked", [False, True])
+def test_sdpa_golden(orc, golden, name, masked):
+    # scaled_dot_product_attention (rpl_attention.c:16-111) on the reference
+    # build's inputs, bit for bit.
+    Q, K, V = golden[f"att_{name}_Q"], golden[f"att_{name}_K"], golden[f"att_{name}_V"]
+    out = orc.sdpa(Q, K, V, golden[f"att_{name}_mask"] if masked else None)
+    assert bits_equal(out, golden[f"att_{name}_out{'_m' if masked else ''}"])
+
+
+def test_sdpa_mathematics(orc):
+    rng = np.random.default_rng(7)
+    B, Sq, Sk, dk, dv = 2, 9, 13, 16, 5
+    Q = rng.standard_normal((B, Sq, dk)).astype(np.float32)
+    K = rng.standard_normal((B, Sk, dk)).astype(np.float32)
+    # Every key carries the same value row: the weights sum to 1, so the
+    # output is that row (within a few ulp).
+    V = np.broadcast_to(rng.standard_normal(dv).astype(np.float32), (B, Sk, dv)).copy()
+    assert np.allclose(orc.sdpa(Q, K, V), V[:, :1, :], rtol=1e-6, atol=1e-6)
+    # Q = 0: equal scores, uniform weights: the mean of V over the keys.
+    V = rng.standard_normal((B, Sk, dv)).astype(np.float32)
+    mean = V.astype(np.float64).mean(1, keepdims=True)
+    assert np.allclose(orc.sdpa(np.zeros_like(Q), K, V), mean, rtol=1e-5, atol=1e-6)
+    # Masked keys (-1e9 before the softmax) get weight exactly 0: changing
+    # their values leaves the output bit-identical.
+    mask = np.ones((B, Sq, Sk), np.float32)
+    mask[:, :, 3] = 0.0
+    V2 = V.copy()
+    V2[:, 3, :] = 1e3
+    assert bits_equal(orc.sdpa(Q, K, V, mask), orc.sdpa(Q, K, V2, mask))
