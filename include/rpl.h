@@ -56,6 +56,19 @@ typedef struct Tensor {
     void (*backward_fn)(struct Tensor*);
 } Tensor;
 
+/* include/rpl.h:80-92 */
+typedef uint16_t rpl_half;
+typedef struct HalfTensor {
+    rpl_half* data;
+    uint32_t dims;
+    uint32_t shape[MAX_DIMS];
+    uint32_t strides[MAX_DIMS];
+    uint32_t size;
+    void* _allocation;
+    DeviceType device;
+    uint32_t gpu_buffer;
+} HalfTensor;
+
 /* include/rpl.h:167-174 */
 typedef struct {
     int8_t* data;
@@ -163,6 +176,23 @@ void backward_mse(Tensor* t);
 Linear* linear_create(uint32_t in_features, uint32_t out_features);
 Tensor* linear_forward(Linear* layer, const Tensor* input);
 void linear_free(Linear* layer);
+
+/* ---- FP16 codec (include/rpl.h:117-119, src/rpl_half.c), bit-exact with
+ * the reference: float -> half truncates and flushes subnormals; the result
+ * of tensor_to_half always holds its values in host memory. ---- */
+HalfTensor* tensor_to_half(const Tensor* t);
+Tensor* tensor_from_half(const HalfTensor* t);
+void half_tensor_free(HalfTensor* t);
+
+/* ---- QAT fake quantization (src/rpl_quantization.c:170-260; exported
+ * there, not declared in the reference header).  Layout:
+ * { Tensor* scale; Tensor* zero_point; bool training;
+ *   uint32_t num_batches_tracked; } ---- */
+typedef struct FakeQuantize FakeQuantize;
+FakeQuantize* fake_quantize_create(void);
+Tensor* fake_quantize_forward(FakeQuantize* fq, const Tensor* input);
+void backward_fake_quant(Tensor* t);
+void fake_quantize_free(FakeQuantize* fq);
 
 /* ---- attention (src/rpl_attention.c:16-111; exported there, not declared
  * in the reference header): Q [B,Sq,dk], K [B,Sk,dk], V [B,Sk,dv], mask

@@ -197,6 +197,15 @@ int rplhip_gelu(const float* x, float* y, uint64_t n, rplhip_stream_t stream);
  * B*Sq*Sk-float workspace. */
 int rplhip_attention(const float* Q, const float* K, const float* V, const float* mask, float* out,
                      uint32_t B, uint32_t Sq, uint32_t Sk, uint32_t dk, uint32_t dv, rplhip_stream_t stream);
+/* fake_quantize_forward's elementwise step (src/rpl_quantization.c:226-233),
+ * DEVICE pointers: y = (clamp(roundf(x * (1/scale) + zp), -128, 127) - zp)
+ * * scale, bit-exact with the reference (its fused multiply-add included). */
+int rplhip_fake_quant(const float* x, float* y, uint64_t n, float scale, float zero_point, rplhip_stream_t stream);
+/* The FP16 codec of src/rpl_half.c:10-75, DEVICE pointers, bit-exact:
+ * float -> half truncates, flushes subnormals to zero and overflows to inf;
+ * half -> float flushes subnormal halves to zero. */
+int rplhip_float_to_half(const float* x, uint16_t* h, uint64_t n, rplhip_stream_t stream);
+int rplhip_half_to_float(const uint16_t* h, float* x, uint64_t n, rplhip_stream_t stream);
 /* optimizer_sgd_step (src/rpl_training.c:70-114) on one parameter tensor of
  * n floats, all DEVICE pointers: weight decay and Nesterov update grad in
  * place as the reference does; velocity (the momentum buffer) may be NULL

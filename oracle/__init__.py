@@ -45,6 +45,9 @@ PROTOTYPES = {
     "orc_tanh": (None, [_vp, _vp, _u32]),
     "orc_gelu": (None, [_vp, _vp, _u32]),
     "orc_sdpa": (None, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32]),
+    "orc_float_to_half": (None, [_vp, _vp, _u32]),
+    "orc_half_to_float": (None, [_vp, _vp, _u32]),
+    "orc_fake_quant": (None, [_vp, _vp, _u32, _vp, _vp, _b]),
 }
 
 
@@ -223,6 +226,26 @@ class Oracle:
         out = np.empty((B, Sq, dv), np.float32)
         self.lib.orc_sdpa(_p(Q), _p(K), _p(V), None if m is None else _p(m), _p(out), B, Sq, Sk, dk, dv)
         return out
+
+    def float_to_half(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        h = np.empty(x.shape, np.uint16)
+        self.lib.orc_float_to_half(_p(x), _p(h), x.size)
+        return h
+
+    def half_to_float(self, h):
+        h = np.ascontiguousarray(h, np.uint16)
+        x = np.empty(h.shape, np.float32)
+        self.lib.orc_half_to_float(_p(h), _p(x), h.size)
+        return x
+
+    def fake_quant(self, x, scale, zp, training):
+        """Returns (y, scale, zp) after one fake_quantize_forward."""
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        s, z = np.float32([scale]), np.float32([zp])
+        self.lib.orc_fake_quant(_p(x), _p(y), x.size, _p(s), _p(z), bool(training))
+        return y, s[0], z[0]
 
     def mlp_step(self, X, Y, W1, b1, W2, b2):
         X, Y, W1, b1, W2, b2 = (np.ascontiguousarray(v, np.float32) for v in (X, Y, W1, b1, W2, b2))

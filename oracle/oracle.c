@@ -433,3 +433,73 @@ void orc_sdpa(const float* Q, const float* K, const float* V, const float* mask,
     }
     free(scores);
 }
+
+/* float_to_half_impl (rpl_half.c:10-42): truncating, subnormal results and
+ * inputs flush to zero, overflow to infinity, NaN -> 0x7e00 | sign. */
+void orc_float_to_half(const float* x, uint16_t* h, uint32_t n) {
+    for (uint32_t i = 0; i < n; i++) {
+        uint32_t f;
+        memcpy(&f, &x[i], 4);
+        uint32_t sign = (f >> 31) & 0x01, exp = (f >> 23) & 0xFF, mant = f & 0x7FFFFF;
+        uint16_t h_sign = (uint16_t)(sign << 15), h_exp = 0, h_mant = 0;
+        if (exp == 255) {
+            h_exp = 31;
+            h_mant = mant ? 0x200 : 0;
+        } else if (exp != 0) {
+            int new_exp = (int)exp - 127 + 15;
+            if (new_exp >= 31) {
+                h_exp = 31;
+            } else if (new_exp > 0) {
+                h_exp = (uint16_t)new_exp;
+                h_mant = (uint16_t)(mant >> 13);
+            }
+        }
+        h[i] = (uint16_t)(h_sign | (h_exp << 10) | h_mant);
+    }
+}
+
+/* half_to_float_impl (rpl_half.c:44-75): subnormal halves -> 0. */
+void orc_half_to_float(const uint16_t* h, float* x, uint32_t n) {
+    for (uint32_t i = 0; i < n; i++) {
+        uint32_t sign = (h[i] >> 15) & 0x01, exp = (h[i] >> 10) & 0x1F, mant = h[i] & 0x3FF;
+        uint32_t f_exp, f_mant;
+        if (exp == 31) {
+            f_exp = 255;
+            f_mant = mant ? 0x7FFFFF : 0;
+        } else if (exp == 0) {
+            f_exp = 0;
+            f_mant = 0;
+        } else {
+            f_exp = exp + 127 - 15;
+            f_mant = mant << 13;
+        }
+        uint32_t f = (sign << 31) | (f_exp << 23) | f_mant;
+        memcpy(&x[i], &f, 4);
+    }
+}
+
+/* fake_quantize_forward (rpl_quantization.c:195-237) on raw arrays, with the
+ * FakeQuantize state as scale / zp in-out: the same expression shapes. */
+void orc_fake_quant(const float* x, float* y, uint32_t n, float* scale_io, float* zp_io, bool training) {
+    float scale = *scale_io, zp = *zp_io;
+    if (training) {
+        float min_val = FLT_MAX, max_val = -FLT_MAX;
+        for (uint32_t i = 0; i < n; i++) {
+            if (x[i] < min_val) min_val = x[i];
+            if (x[i] > max_val) max_val = x[i];
+        }
+        float new_scale = (max_val - min_val) / 255.0f;
+        float new_zp = -min_val / new_scale;
+        float momentum = 0.1f;
+        scale = (1.0f - momentum) * scale + momentum * new_scale;
+        zp = (1.0f - momentum) * zp + momentum * new_zp;
+        *scale_io = scale;
+        *zp_io = zp;
+    }
+    float inv_scale = 1.0f / scale;
+    for (uint32_t i = 0; i < n; i++) {
+        int32_t q = (int32_t)roundf(x[i] * inv_scale + zp);
+        q = (q < -128) ? -128 : (q > 127 ? 127 : q);
+        y[i] = (q - zp) * scale;
+    }
+}

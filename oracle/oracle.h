@@ -130,6 +130,12 @@ void orc_gelu(const float* x, float* y, uint32_t n);
 void orc_sdpa(const float* Q, const float* K, const float* V, const float* mask, float* out, uint32_t B,
               uint32_t Sq, uint32_t Sk, uint32_t dk, uint32_t dv);
 
+/* rpl_half.c:10-75 */
+void orc_float_to_half(const float* x, uint16_t* h, uint32_t n);
+void orc_half_to_float(const uint16_t* h, float* x, uint32_t n);
+/* rpl_quantization.c:195-237 */
+void orc_fake_quant(const float* x, float* y, uint32_t n, float* scale_io, float* zp_io, bool training);
+
 #ifdef __cplusplus
 }
 #endif

@@ -108,6 +108,32 @@ class Linear(C.Structure):
     ]
 
 
+class HalfTensor(C.Structure):
+    """Reference include/rpl.h:82-92."""
+
+    _fields_ = [
+        ("data", C.POINTER(C.c_uint16)),
+        ("dims", C.c_uint32),
+        ("shape", C.c_uint32 * 8),
+        ("strides", C.c_uint32 * 8),
+        ("size", C.c_uint32),
+        ("_allocation", C.c_void_p),
+        ("device", C.c_int),
+        ("gpu_buffer", C.c_uint32),
+    ]
+
+
+class FakeQuantize(C.Structure):
+    """Reference src/rpl_quantization.c:174-179 (file-local there)."""
+
+    _fields_ = [
+        ("scale", C.POINTER(Tensor)),
+        ("zero_point", C.POINTER(Tensor)),
+        ("training", C.c_bool),
+        ("num_batches_tracked", C.c_uint32),
+    ]
+
+
 class Optimizer(C.Structure):
     """Reference src/rpl_training.c:20-28 (opaque in include/rpl.h)."""
 
@@ -182,6 +208,9 @@ PROTOTYPES = {
     "rplhip_tanh": (_int, [_vp, _vp, _u64, _vp]),
     "rplhip_gelu": (_int, [_vp, _vp, _u64, _vp]),
     "rplhip_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
+    "rplhip_fake_quant": (_int, [_vp, _vp, _u64, _f32, _f32, _vp]),
+    "rplhip_float_to_half": (_int, [_vp, _vp, _u64, _vp]),
+    "rplhip_half_to_float": (_int, [_vp, _vp, _u64, _vp]),
     "rplhip_fill": (_int, [_vp, _u64, _f32, _vp]),
     # ---- rpl.h
     "tensor_create": (_PT, [_u32, C.POINTER(_u32), C.c_bool]),
@@ -235,6 +264,13 @@ PROTOTYPES = {
     "optimizer_sgd_create": (C.POINTER(Optimizer), [C.POINTER(_PT), _u32, _f32, _f32, _f32, _f32, C.c_bool]),
     "optimizer_sgd_step": (None, [C.POINTER(Optimizer)]),
     "scaled_dot_product_attention": (_PT, [_PT, _PT, _PT, _PT, _f32, C.c_bool]),
+    "tensor_to_half": (C.POINTER(HalfTensor), [_PT]),
+    "tensor_from_half": (_PT, [C.POINTER(HalfTensor)]),
+    "half_tensor_free": (None, [C.POINTER(HalfTensor)]),
+    "fake_quantize_create": (C.POINTER(FakeQuantize), []),
+    "fake_quantize_forward": (_PT, [C.POINTER(FakeQuantize), _PT]),
+    "backward_fake_quant": (None, [_PT]),
+    "fake_quantize_free": (None, [C.POINTER(FakeQuantize)]),
     "rpl_last_error": (C.c_char_p, []),
     "rpl_clear_last_error": (None, []),
     "rpl_gpu_synchronize": (None, []),

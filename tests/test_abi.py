@@ -53,6 +53,10 @@ def test_struct_layouts_match_reference():
     assert (O.learning_rate.offset, O.weight_decay.offset, O.num_params.offset, O.parameters.offset,
             O.state.offset, C.sizeof(O)) == (4, 8, 12, 16, 24, 32)
     assert (S.dampening.offset, S.nesterov.offset, S.velocity.offset, C.sizeof(S)) == (4, 8, 16, 24)
+    # include/rpl.h:82-92 and src/rpl_quantization.c:174-179.
+    H, F = rpl_amd.HalfTensor, rpl_amd.FakeQuantize
+    assert (H.dims.offset, H.size.offset, H._allocation.offset, H.device.offset, C.sizeof(H)) == (8, 76, 80, 88, 96)
+    assert (F.training.offset, F.num_batches_tracked.offset, C.sizeof(F)) == (16, 20, 24)
 
 
 def test_no_device_fails_loudly(rpl):

@@ -399,3 +399,38 @@ def test_sdpa_mathematics(orc):
     V2 = V.copy()
     V2[:, 3, :] = 1e3
     assert bits_equal(orc.sdpa(Q, K, V, mask), orc.sdpa(Q, K, V2, mask))
+
+
+def test_half_codec_golden(orc, golden):
+    # rpl_half.c:10-75: every half, and the float sweep, bit for bit.
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    assert bits_equal(orc.half_to_float(h), golden["half_all_f32"])
+    assert np.array_equal(orc.float_to_half(golden["half_from_f32_x"]), golden["half_from_f32_h"])
+
+
+def test_half_codec_closed_forms(orc):
+    # Normal halves survive the round trip exactly; floats are truncated
+    # (1 + 2^-11 -> 1, 65519.99 -> 65504), >= 65536 overflows to inf,
+    # subnormal results flush to signed zero.
+    h = np.array([0x3C00, 0x7BFF, 0x0400, 0xC2AA, 0x8401], np.uint16)
+    assert np.array_equal(orc.float_to_half(orc.half_to_float(h)), h)
+    x = np.float32([1 + 2 ** -11, 65519.99, 65536.0, -1e10, 2 ** -15, -2 ** -20, np.inf])
+    assert np.array_equal(orc.float_to_half(x), np.array([0x3C00, 0x7BFF, 0x7C00, 0xFC00, 0x0000, 0x8000, 0x7C00],
+                                                         np.uint16))
+
+
+def test_fake_quant_golden(orc, golden):
+    # fake_quantize_forward (rpl_quantization.c:195-237): outputs and the
+    # moving-average state after two training steps and one eval step.
+    s, z = np.float32(1.0), np.float32(0.0)
+    for step in range(3):
+        y, s, z = orc.fake_quant(golden[f"fq_{step}_x"], s, z, bool(golden[f"fq_{step}_state"][2]))
+        assert bits_equal(y, golden[f"fq_{step}_y"])
+        assert bits_equal(np.float32([s, z]), golden[f"fq_{step}_state"][:2])
+
+
+def test_fake_quant_closed_form(orc):
+    # scale 1, zero point 0, eval: y = clamp(roundf(x), -128, 127), ties away.
+    x = np.float32([0.5, -0.5, 1.5, 2.5, -2.5, 126.6, 300.0, -300.0, 0.49999997])
+    y, s, z = orc.fake_quant(x, 1.0, 0.0, False)
+    assert np.array_equal(y, np.float32([1, -1, 2, 3, -3, 127, 127, -128, 0])) and (s, z) == (1.0, 0.0)
