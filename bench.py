@@ -8,7 +8,9 @@ same way and reported beside it.  Inputs are generated from fixed seeds,
 uploaded and quantized before the timed region (resident in HBM).
 
 `value` is the INT8 throughput in TOP/s.  `roofline` covers the dominant
-kernel (the i8-MFMA GEMM kernel, timed alone with HIP events on its stream);
+kernel: gemm_int8 is one launch of the i8-MFMA GEMM kernel that reads B
+[K,N] in place, timed alone with HIP events on its stream (`nt_kernel`
+times the same kernel on B already [N,K], linear_int8's layout);
 `cpu_baseline` times the C oracle (a bit-identical restatement of the
 reference's CPU path) on a 64-row slab of the same INT8 GEMM on the host's
 cores.  Prints ONE JSON line.
@@ -263,7 +265,7 @@ def main():
     ap.add_argument("--settle-ms", type=float, default=300.0,
                     help="untimed gemm_int8 work before the first timed leg: the first ~100 ms of load on an idle "
                          "MI355X run at boost clock and then through a power-management dip")
-    ap.add_argument("--only", choices=["int8", "int8-kernel", "fp32", "skinny", "configs"],
+    ap.add_argument("--only", choices=["int8", "int8-kernel", "int8-nt", "fp32", "skinny", "configs"],
                     help="run one leg only (for profiling); the JSON line then has nulls for the rest")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -313,13 +315,20 @@ def main():
         ms_i8, wall_i8 = timer.time(int8_step, args.steps, args.warmup)
         tops = ops / (ms_i8 * 1e-3) / 1e12
 
-    # Dominant kernel alone: the i8-MFMA GEMM on B already in [N,K] (what
-    # gemm_int8 runs after its transpose pass).
-    kern = lambda: check(lib.rplhip_linear_int8(qA.ptr, qB.ptr, None, dC.ptr, n, n, n, stream))  # noqa: E731
+    # Dominant kernel alone: gemm_int8 launches exactly one kernel
+    # (k_gemm_i8_nt_dma with B [K,N] read in place), timed on its stream.
     if want("int8-kernel") or args.only is None:
         log("bench: int8 GEMM kernel alone")
-        ms_k, _ = timer.time(kern, args.steps, args.warmup)
+        ms_k, _ = timer.time(int8_step, args.steps, args.warmup)
         kern_tops = ops / (ms_k * 1e-3) / 1e12
+    # The same kernel on B already [N,K] (linear_int8's layout, raw int32).
+    nt = None
+    if want("int8-nt") or args.only is None:
+        log("bench: int8 NT kernel (linear_int8)")
+        ms_nt, _ = timer.time(lambda: check(lib.rplhip_linear_int8(qA.ptr, qB.ptr, None, dC.ptr, n, n, n, stream)),
+                              args.steps, args.warmup)
+        nt = {"kernel": "k_gemm_i8_nt_dma<0, 256>", "ms_per_launch": round(ms_nt, 4),
+              "achieved": round(ops / (ms_nt * 1e-3) / 1e12, 2), "unit": "TOP/s"}
 
     # ---- FP32 8192^3 NN (tensor_gemm semantics, alpha=1, beta=0)
     dCf = DeviceBuffer(n * n * 4)
@@ -407,11 +416,11 @@ def main():
 
     # HBM/MALL bytes per launch of the roofline kernel, from the committed
     # FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel of known size).
-    traffic, traffic_kernel = None, "k_gemm_i8_nt_dma<0>"
+    traffic, traffic_kernel = None, "k_gemm_i8_nt_dma<4, 256, true>"
     tpath = os.path.join(REPO, "profiles", "traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            rec = json.load(f).get("gemm_i8_nt_8192", {})
+            rec = json.load(f).get("gemm_int8_8192", {})
         traffic, traffic_kernel = rec.get("bytes_per_launch"), rec.get("kernel", traffic_kernel)
 
     out = {
@@ -436,6 +445,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(kern_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": round(kern_tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
                      "kernel": traffic_kernel, "ms_per_launch": round(ms_k, 4)},
+        "nt_kernel": nt,
         "roofline_fp32": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4), "kernel": "k_sgemm"},
         "skinny_int8": skinny,

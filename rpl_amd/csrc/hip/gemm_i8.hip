@@ -509,6 +509,20 @@ __device__ __forceinline__ void epilogue_tile_full(const EpiParams& p, const v16
 
 namespace dma {
 constexpr int BM = 256, BK = 64, S = RPL_I8_STAGES, kThreads = 256;
+// [K][N] B tiles: k-row r keeps its logical 16-byte chunk c in physical
+// chunk c ^ kn_swz(r % 8).  The XOR moves chunk bits 0, 1 and 3 and leaves
+// bit 2 alone, so fragments j and j+2 (columns 64 apart) stay 64 bytes apart
+// in every row and share one address register.
+__device__ __forceinline__ uint32_t kn_swz(uint32_t e) { return (e & 3) | ((e & 4) << 1); }
+typedef __attribute__((address_space(3))) v2i* lds_v2i;
+// ds_read_b64_tr_b8 through a restrict parameter: inlining gives the read
+// alias-scope metadata, as the kernel's plain LDS reads have.  Without it
+// the compiler's wait insertion cannot tell the read from the in-flight
+// direct-to-LDS copies and waits for all of them (vmcnt(0)) before every
+// first read of a half, which serialises the copy pipeline.  The copies a
+// read depends on are waited for explicitly (vmcnt + barrier), as for the
+// A fragments.
+__device__ __forceinline__ v2i tr8(lds_v2i __restrict__ p) { return __builtin_amdgcn_ds_read_tr8_b64_v2i32(p); }
 constexpr int kSlot = RPL_I8_DMA_SLOT;
 // B-tile height BN = 256 (the big tile) or 128 (grids with too few 256 x
 // 256 tiles to fill the chip): 4 waves (2 x 2), wave tile 128 x BN/2.
@@ -550,7 +564,20 @@ struct Frags {
 //
 // Requires K % 64 == 0, 16-byte aligned operands and leading dimensions,
 // and operands below 2 GiB (32-bit buffer offsets).
-template <int EPI, int BN>
+//
+// BKN: B is stored [K][N] (row k at B + k*ldb, the layout of gemm_int8's
+// B) and is read in place, with no transposed copy.  A B stage is then 64
+// k-rows of 256 bytes: each copy instruction moves 4 k-rows, lane l writing
+// 16-byte chunk l%16 of row l/16, fetched from logical chunk
+// (l%16) ^ 2*(k%8).  The fragments come from ds_read_b64_tr_b8: within each
+// 16-lane group, lane 2e+h addresses 8 bytes (columns 8h..8h+7 of the
+// group's 16-column chunk) of k-row k0+e, and output lane 8h+b receives
+// byte b of lane 2e+h's piece as its byte e, i.e. column 8h+b at k-rows
+// k0..k0+7.  Two such reads give a lane the 16 k-bytes of its column that
+// the MFMA's B operand holds, in the same k order as the A fragment.  The
+// eight k-rows of one read sit in 8 distinct 16-byte chunks of their rows
+// (dma::kn_swz).  Needs BN = 256, N % 16 == 0.
+template <int EPI, int BN, bool BKN = false>
 __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restrict__ A, uint32_t lda,
                                                            const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
                                                            uint32_t N, uint32_t K, EpiParams p) {
@@ -561,6 +588,7 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
     using G = dma::Geo<BN>;
     constexpr int FN = G::FN, kLoadsA = G::kLoadsA, kLoadsB = G::kLoadsB, kVmPerTile = G::kVmPerTile;
     constexpr int kTileBytesA = G::kTileBytesA, kStageBytes = G::kStageBytes;
+    static_assert(!BKN || BN == 256, "[K][N] B needs 256-column tiles");
     __shared__ __attribute__((aligned(1024))) int8_t smem[S * kStageBytes];
 
     const uint32_t lane = threadIdx.x % 64;
@@ -572,7 +600,10 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
     const uint32_t rows_a = M - m0 < (uint32_t)BM ? M - m0 : BM;
     const uint32_t rows_b = N - n0 < (uint32_t)BN ? N - n0 : BN;
     const __amdgpu_buffer_rsrc_t rsrc_a = uniform_rsrc(A + (uint64_t)m0 * lda, rows_a * lda);
-    const __amdgpu_buffer_rsrc_t rsrc_b = uniform_rsrc(B + (uint64_t)n0 * ldb, rows_b * ldb);
+    // [K][N] B: the resource starts at column n0 and ends after column N-1
+    // of row K-1.
+    const __amdgpu_buffer_rsrc_t rsrc_b = BKN ? uniform_rsrc(B + n0, (K - 1) * ldb + rows_b)
+                                              : uniform_rsrc(B + (uint64_t)n0 * ldb, rows_b * ldb);
 
     // Source offsets of this lane's A and B copies (k added as the scalar
     // offset): wave w copies rows w*BM/4 .. and w*BN/4 .. of the tiles.
@@ -587,8 +618,19 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
     }
 #pragma unroll
     for (int i = 0; i < kLoadsB; i++) {
-        const uint32_t r = wave * (BN / 4) + i * 16 + lane / 4;
-        voff_b[i] = (r < rows_b ? r : rows_b - 1) * ldb + ((lane % 4) ^ swz(r)) * 16;
+        if constexpr (BKN) {
+            // k-row r of the tile; chunks past the last column (N % 256 != 0)
+            // are clamped to the last one, so every load stays inside B.
+            // Copies i and i+2 are 8 k-rows apart with the same chunks: the
+            // 8 rows go in the scalar offset, so only i = 0, 1 take VGPRs.
+            if (i >= 2) continue;
+            const uint32_t r = wave * 16 + i * 4 + lane / 16;
+            const uint32_t c = (lane % 16) ^ dma::kn_swz(r % 8);
+            voff_b[i] = r * ldb + (16 * c < rows_b ? c : rows_b / 16 - 1) * 16;
+        } else {
+            const uint32_t r = wave * (BN / 4) + i * 16 + lane / 4;
+            voff_b[i] = (r < rows_b ? r : rows_b - 1) * ldb + ((lane % 4) ^ swz(r)) * 16;
+        }
     }
     auto issue_a = [&](uint32_t kt, uint32_t stage) {
         int8_t* st = smem + stage * kStageBytes;
@@ -602,7 +644,8 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
 #pragma unroll
         for (int i = 0; i < kLoadsB; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rsrc_b, (lds_ptr)(st + kTileBytesA + (wave * (BN / 4) + i * 16) * BK), 16, voff_b[i], kt * BK, 0, 0);
+                rsrc_b, (lds_ptr)(st + kTileBytesA + (wave * (BN / 4) + i * 16) * BK), 16, voff_b[BKN ? i % 2 : i],
+                BKN ? (kt * BK + 8 * (i / 2)) * ldb : kt * BK, 0, 0);
     };
     auto issue = [&](uint32_t kt, uint32_t stage) {
         issue_a(kt, stage);
@@ -625,13 +668,35 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
 #pragma unroll
     for (int kk = 0; kk < 2; kk++) foff[kk] = fr * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
     const uint32_t a_base = wm * 128 * BK, b_base = kTileBytesA + wn * (BN / 2) * BK;
+    // [K][N] B: lane 16g + 2e + h reads k-row 16(g/2) + e (+ 32kk + 8t) at
+    // columns 128wn + 32j + 16(g%2) + 8h, in chunk
+    // (8wn + 2j + g%2) ^ kn_swz(e); fragments j and j+2 are 64 bytes apart.
+    uint32_t boff[2];
+    if constexpr (BKN) {
+        const uint32_t g = lane / 16, e = (lane % 16) / 2, h = lane % 2;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            boff[j] = kTileBytesA + (16 * (g / 2) + e) * 256 + ((8 * wn + 2 * j + g % 2) ^ dma::kn_swz(e)) * 16 + 8 * h;
+    }
     using F = dma::Frags<FN>;
+    using dma::lds_v2i;
     auto fload = [&](uint32_t stage, int kk, F& f) {
         const int8_t* st = smem + stage * kStageBytes + foff[kk];
 #pragma unroll
         for (int i = 0; i < 4; i++) f.a[i] = *reinterpret_cast<const v4i*>(st + a_base + i * 32 * BK);
+        if constexpr (BKN) {
+            const int8_t* sb = smem + stage * kStageBytes + kk * 32 * 256;
 #pragma unroll
-        for (int j = 0; j < FN; j++) f.b[j] = *reinterpret_cast<const v4i*>(st + b_base + j * 32 * BK);
+            for (int j = 0; j < FN; j++) {
+                const int8_t* pb = sb + boff[j % 2] + 64 * (j / 2);
+                const v2i lo = dma::tr8((lds_v2i)pb);
+                const v2i hi = dma::tr8((lds_v2i)(pb + 8 * 256));
+                f.b[j] = (v4i){lo.x, lo.y, hi.x, hi.y};
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < FN; j++) f.b[j] = *reinterpret_cast<const v4i*>(st + b_base + j * 32 * BK);
+        }
     };
     v16i acc[4][4];
 #pragma unroll
@@ -650,7 +715,7 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
     // copies: the last two MFMAs take two copies each).
     auto pin = [&](auto copies_c) {
         constexpr int copies = decltype(copies_c)::value;
-        if constexpr (FN == 4) {
+        if constexpr (FN == 4 && !BKN) {
             static_for<8>([&](auto) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
@@ -660,7 +725,7 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // HBM -> LDS copy
             });
         } else {
-            constexpr int reads = 4 + FN, rest = 4 * FN - reads;
+            constexpr int reads = 4 + (BKN ? 2 : 1) * FN, rest = 4 * FN - reads;
             static_for<reads>([&](auto) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
@@ -1435,6 +1500,29 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
     return launch_nt<CfgSmall, EPI>(A, lda, B, ldb, M, N, K, p, al, s);
 }
 
+// B stored [K][N] (gemm_int8's layout, ldb = N) read in place by the
+// direct-to-LDS kernel: shapes that take its 256 x 256 tile, N % 16 == 0.
+// RPLHIP_I8_KN=0 sends them through the transposed copy instead (for A/B
+// timing only).
+bool kn_ok(const int8_t* A, const int8_t* B, uint32_t M, uint32_t N, uint32_t K) {
+    static const char* env = getenv("RPLHIP_I8_KN");
+    if (env && env[0] == '0') return false;
+    if (RPL_I8_BIG_KERNEL == 1 || M <= 16 || K == 0 || K % dma::BK || N % 16 || !aligned16(A) || !aligned16(B))
+        return false;
+    if ((uint64_t)M * K >= (1ull << 31) || (uint64_t)K * N >= (1ull << 31)) return false;
+    const uint64_t tiles = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
+    return use_dma() && use_big_tile(M, N, true) && tiles <= 0x7fffffffull;
+}
+
+template <int EPI>
+int launch_kn(const int8_t* A, const int8_t* B, uint32_t M, uint32_t N, uint32_t K, const EpiParams& p,
+              hipStream_t s) {
+    const uint32_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+    hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256, true>), dim3(tiles), dim3(dma::kThreads), 0, s, A, K, B, N, M, N,
+                       K, p);
+    return rplhip::check_launch("int8 GEMM ([K][N] B)");
+}
+
 // True (and *inv = 1/sc) when sc = +-2^k is a normal float whose reciprocal
 // is exactly representable: then x / sc and x * (1/sc) are both the
 // correctly rounded value of the same real number, for every x (overflow,
@@ -1510,7 +1598,10 @@ int rplhip_gemm_int8(const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, u
     if (!C || (K && (!A || !B))) return fail(RPLHIP_ERR_INVALID, "rplhip_gemm_int8: NULL pointer");
     RPLHIP_REQUIRE_DEVICE();
     hipStream_t s = as_stream(stream);
-    size_t bt_bytes = ((size_t)K * N + 15) / 16 * 16;
+    // B is read in place when the kernel can (the column sums of a zero
+    // point of B come from the transposed copy).
+    const bool kn = za == 0 && kn_ok(A, B, M, N, K);
+    size_t bt_bytes = kn ? 0 : ((size_t)K * N + 15) / 16 * 16;
     size_t sums = (za ? (size_t)N : 0) + (zb ? (size_t)M : 0);
     void* ws = nullptr;
     int st = ws_alloc(&ws, bt_bytes + sizeof(int32_t) * sums + 16, s);
@@ -1526,7 +1617,7 @@ int rplhip_gemm_int8(const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, u
     p.za = za;
     p.zb = zb;
     p.kzz = (int32_t)((uint32_t)K * (uint32_t)za * (uint32_t)zb);
-    if (K) st = transpose_b(B, K, N, Bt, s);
+    if (K && !kn) st = transpose_b(B, K, N, Bt, s);
     if (!st && zb && K) {
         p.rowsum_a = sum_ptr;
         sum_ptr += M;
@@ -1540,11 +1631,11 @@ int rplhip_gemm_int8(const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, u
     }
     if (!st) {
         if (za == 0 && zb == 0 && sc == 1.0f && requant_in_range(K, sa, sb))
-            st = run_nt<kRequantUnit>(A, K, Bt, K, M, N, K, p, s);
+            st = kn ? launch_kn<kRequantUnit>(A, B, M, N, K, p, s) : run_nt<kRequantUnit>(A, K, Bt, K, M, N, K, p, s);
         else if (za == 0 && zb == 0 && exact_reciprocal(sc, &p.inv_sc))
-            st = run_nt<kRequantPow2>(A, K, Bt, K, M, N, K, p, s);
+            st = kn ? launch_kn<kRequantPow2>(A, B, M, N, K, p, s) : run_nt<kRequantPow2>(A, K, Bt, K, M, N, K, p, s);
         else
-            st = run_nt<kRequant>(A, K, Bt, K, M, N, K, p, s);
+            st = kn ? launch_kn<kRequant>(A, B, M, N, K, p, s) : run_nt<kRequant>(A, K, Bt, K, M, N, K, p, s);
     }
     ws_free(ws, s);
     return st;
@@ -1558,9 +1649,6 @@ int rplhip_gemm_int8_dequant(const int8_t* A, const float* a_scale, int a_per_ro
         return fail(RPLHIP_ERR_INVALID, "rplhip_gemm_int8_dequant: NULL pointer");
     RPLHIP_REQUIRE_DEVICE();
     hipStream_t s = as_stream(stream);
-    void* ws = nullptr;
-    int st = ws_alloc(&ws, ((size_t)K * N + 15) / 16 * 16 + 16, s);
-    if (st) return st;
     EpiParams p = {};
     p.sx = a_scale;
     p.sw = b_scale;
@@ -1568,6 +1656,10 @@ int rplhip_gemm_int8_dequant(const int8_t* A, const float* a_scale, int a_per_ro
     p.sw_per_col = b_per_col;
     p.out_f32 = Y;
     p.ldc = N;
+    if (kn_ok(A, B, M, N, K)) return launch_kn<kDequant>(A, B, M, N, K, p, s);
+    void* ws = nullptr;
+    int st = ws_alloc(&ws, ((size_t)K * N + 15) / 16 * 16 + 16, s);
+    if (st) return st;
     if (K) st = transpose_b(B, K, N, (int8_t*)ws, s);
     if (!st) st = run_nt<kDequant>(A, K, (const int8_t*)ws, K, M, N, K, p, s);
     ws_free(ws, s);

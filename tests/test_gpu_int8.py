@@ -225,10 +225,12 @@ def _requant_f32(acc, sa, sb, sc):
 # (k_gemm_i8_nt_dma); K = 448 and 832 run its steady-state loop and tails of
 # 3 and 5 tiles.  The first two shapes have ragged edges in M and N, so both
 # the bounds-checked epilogue (edge tiles) and the unchecked buffer-store
-# epilogue (interior tiles) run; gemm_int8 transposes B [K,N] first.
-# (1800, 3000, 448) has too few 256 x 256 tiles and takes 256 x 128 ones
-# (192 of them), with ragged M and N edges.
-BIG = [(5890, 5900, 832), (5890, 5888, 832), (6144, 6144, 448), (1800, 3000, 448)]
+# epilogue (interior tiles) run.  gemm_int8 and gemm_int8_dequant read B
+# [K,N] in place when N % 16 == 0 (5888, 6144, 4400; at N = 4400 the last
+# tile holds 48 columns and the chunks past them are clamped), and transpose
+# it first otherwise (5900, 3000).  (1800, 3000, 448) has too few 256 x 256
+# tiles and takes 256 x 128 ones (192 of them), with ragged M and N edges.
+BIG = [(5890, 5900, 832), (5890, 5888, 832), (6144, 6144, 448), (1800, 3000, 448), (2900, 4400, 448)]
 
 
 @pytest.mark.parametrize("M,N,K", BIG)
