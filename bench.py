@@ -327,7 +327,7 @@ def main():
         log("bench: int8 NT kernel (linear_int8)")
         ms_nt, _ = timer.time(lambda: check(lib.rplhip_linear_int8(qA.ptr, qB.ptr, None, dC.ptr, n, n, n, stream)),
                               args.steps, args.warmup)
-        nt = {"kernel": "k_gemm_i8_nt_dma<0, 256>", "ms_per_launch": round(ms_nt, 4),
+        nt = {"kernel": "k_gemm_i8_dma_pairs<0, false>", "ms_per_launch": round(ms_nt, 4),
               "achieved": round(ops / (ms_nt * 1e-3) / 1e12, 2), "unit": "TOP/s"}
 
     # ---- FP32 8192^3 NN (tensor_gemm semantics, alpha=1, beta=0)
@@ -416,7 +416,7 @@ def main():
 
     # HBM/MALL bytes per launch of the roofline kernel, from the committed
     # FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel of known size).
-    traffic, traffic_kernel = None, "k_gemm_i8_nt_dma<4, 256, true>"
+    traffic, traffic_kernel = None, "k_gemm_i8_dma_pairs<4, true>"
     tpath = os.path.join(REPO, "profiles", "traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:

@@ -803,6 +803,220 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
                                      N);
 }
 
+// ------------------- big-tile GEMM with A copied two k-steps at a time
+
+// Same tile, MFMA, B path and epilogues as k_gemm_i8_nt_dma<EPI, 256, BKN>,
+// with A copied in k-step pairs: one copy instruction moves 8 rows x 128
+// bytes (8 whole cache lines; the per-k-step copy moves 16 rows x 64 bytes,
+// half of 16 lines, and fetches each line twice).  A pair of A tiles fills a
+// 32 KB region laid out in 1 KB row groups: group g holds rows 8g..8g+7, the
+// first 512 bytes k-step 2p, the next 512 bytes k-step 2p+1, each as 8 rows
+// x 64 bytes with chunk c at slot c ^ swz(row % 8).  Lane l of a copy writes
+// bytes 16l..16l+15 of one group, so it fetches k-step l/32, row (l%32)/4,
+// chunk (l%4) ^ swz(row).  Fragment reads then see the per-k-step layout
+// (64-byte rows, the same swizzle) at a parity offset of 0 or 512 bytes.
+//
+// LDS: two A pair regions (64 KB) and four B stages (64 KB).  Iteration j
+// requests A pair (j+2, j+3) at its start when j is even, and B tile j+3
+// after its barrier; at the barrier a wave has issued, after the copies of
+// tile j+1 it waits for, 4 B + 8 A copies (j even) or 4 B copies (j odd).
+// Requires K % 128 == 0 (plus the conditions of k_gemm_i8_nt_dma).
+namespace dma {
+constexpr int kPairBytes = BM * 2 * BK;  // 256 rows x 128 k-bytes
+constexpr int kPairLoads = 8;            // 1 KB copies per wave per A pair
+}  // namespace dma
+
+template <int EPI, bool BKN>
+__global__ void __launch_bounds__(256, 1) k_gemm_i8_dma_pairs(const int8_t* __restrict__ A, uint32_t lda,
+                                                              const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
+                                                              uint32_t N, uint32_t K, EpiParams p) {
+    using dma::BK;
+    using dma::BM;
+    using dma::kPairBytes;
+    using dma::kPairLoads;
+    constexpr int BN = 256, S = 4;
+    using G = dma::Geo<BN>;
+    constexpr int FN = G::FN, kLoadsB = G::kLoadsB;
+    constexpr int kBStage = BN * BK, kBBase = 2 * kPairBytes;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kBBase + S * kBStage];
+
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t wm = wave / 2, wn = wave % 2;
+    uint32_t im, in;
+    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, im, in);
+    const uint32_t m0 = im * BM, n0 = in * BN;
+    const uint32_t rows_a = M - m0 < (uint32_t)BM ? M - m0 : BM;
+    const uint32_t rows_b = N - n0 < (uint32_t)BN ? N - n0 : BN;
+    const __amdgpu_buffer_rsrc_t rsrc_a = uniform_rsrc(A + (uint64_t)m0 * lda, rows_a * lda);
+    const __amdgpu_buffer_rsrc_t rsrc_b = BKN ? uniform_rsrc(B + n0, (K - 1) * ldb + rows_b)
+                                              : uniform_rsrc(B + (uint64_t)n0 * ldb, rows_b * ldb);
+
+    // A pair copies: wave w fills row groups 8w .. 8w+7 (rows 64w .. 64w+63);
+    // copy i covers rows 64w + 8i + a_rr.  Rows past M are clamped to the
+    // last row (never stored).
+    const uint32_t a_rr = (lane % 32) / 4;
+    const uint32_t a_row = wave * 64 + a_rr;
+    const uint32_t a_col = (lane / 32) * BK + ((lane % 4) ^ swz(a_rr)) * 16;
+    auto issue_a_pair = [&](uint32_t pair, int slot) {
+        int8_t* st = smem + slot * kPairBytes + wave * 8 * 1024;
+#pragma unroll
+        for (int i = 0; i < kPairLoads; i++) {
+            const uint32_t r = a_row + 8 * i;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr)(st + i * 1024), 16,
+                                                     (r < rows_a ? r : rows_a - 1) * lda + a_col, pair * 2 * BK, 0,
+                                                     0);
+        }
+    };
+    // B copies as in k_gemm_i8_nt_dma.
+    uint32_t voff_b[4];
+#pragma unroll
+    for (int i = 0; i < kLoadsB; i++) {
+        if constexpr (BKN) {
+            if (i >= 2) continue;
+            const uint32_t r = wave * 16 + i * 4 + lane / 16;
+            const uint32_t c = (lane % 16) ^ dma::kn_swz(r % 8);
+            voff_b[i] = r * ldb + (16 * c < rows_b ? c : rows_b / 16 - 1) * 16;
+        } else {
+            const uint32_t r = wave * (BN / 4) + i * 16 + lane / 4;
+            voff_b[i] = (r < rows_b ? r : rows_b - 1) * ldb + ((lane % 4) ^ swz(r)) * 16;
+        }
+    }
+    auto issue_b = [&](uint32_t kt, uint32_t stage) {
+        int8_t* st = smem + kBBase + stage * kBStage;
+#pragma unroll
+        for (int i = 0; i < kLoadsB; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr)(st + (wave * (BN / 4) + i * 16) * BK), 16,
+                                                     voff_b[BKN ? i % 2 : i],
+                                                     BKN ? (kt * BK + 8 * (i / 2)) * ldb : kt * BK, 0, 0);
+    };
+
+    // Fragment reads.  A: row R = 128wm + 32i + fr lives in group R/8 at
+    // row R%8 = fr%8.  B: as in k_gemm_i8_nt_dma.
+    const uint32_t fr = lane % 32;
+    uint32_t foff_a[2], foff_b[2], boff[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+        foff_a[kk] = wm * 16 * 1024 + (fr / 8) * 1024 + (fr % 8) * BK + ((2 * kk + lane / 32) ^ swz(fr % 8)) * 16;
+        if constexpr (!BKN) foff_b[kk] = wn * (BN / 2) * BK + fr * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
+    }
+    if constexpr (BKN) {
+        const uint32_t g = lane / 16, e = (lane % 16) / 2, h = lane % 2;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            boff[j] = (16 * (g / 2) + e) * 256 + ((8 * wn + 2 * j + g % 2) ^ dma::kn_swz(e)) * 16 + 8 * h;
+    }
+    using F = dma::Frags<FN>;
+    using dma::lds_v2i;
+    // Tile j: A in pair slot (j/2)%2 at parity j%2, B in stage j%4.
+    auto fload = [&](uint32_t aslot, uint32_t par, uint32_t stage, int kk, F& f) {
+        const int8_t* sa = smem + aslot * kPairBytes + par * 512 + foff_a[kk];
+#pragma unroll
+        for (int i = 0; i < 4; i++) f.a[i] = *reinterpret_cast<const v4i*>(sa + i * 4096);
+        if constexpr (BKN) {
+            const int8_t* sb = smem + kBBase + stage * kBStage + kk * 32 * 256;
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int8_t* pb = sb + boff[j % 2] + 64 * (j / 2);
+                const v2i lo = dma::tr8((lds_v2i)pb);
+                const v2i hi = dma::tr8((lds_v2i)(pb + 8 * 256));
+                f.b[j] = (v4i){lo.x, lo.y, hi.x, hi.y};
+            }
+        } else {
+            const int8_t* sb = smem + kBBase + stage * kBStage + foff_b[kk];
+#pragma unroll
+            for (int j = 0; j < FN; j++) f.b[j] = *reinterpret_cast<const v4i*>(sb + j * 32 * BK);
+        }
+    };
+    v16i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = (v16i){};
+    auto mma = [&](const F& f) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+    };
+    // One half's order: a fragment read after each early MFMA, then the
+    // half's copies spread over the remaining MFMAs.
+    auto pin = [&](auto copies_c) {
+        constexpr int copies = decltype(copies_c)::value;
+        constexpr int reads = 4 + (BKN ? 2 : 1) * FN, rest = 4 * FN - reads;
+        static_for<reads>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        });
+        if constexpr (copies > 0) {
+            static_for<rest>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, (copies + rest - 1) / rest, 0);
+            });
+        }
+    };
+
+    const uint32_t nk = K / BK;  // even, >= 2
+    // Prologue: A pair 0, B tiles 0 .. 2; tile 0 landed (B 1, 2 may not).
+    issue_a_pair(0, 0);
+    issue_b(0, 0);
+    issue_b(1, 1);
+    if (nk > 2) {
+        issue_b(2, 2);
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kLoadsB, 0));
+    } else {
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLoadsB, 0));
+    }
+    __builtin_amdgcn_s_barrier();
+    F f0, f1;
+    fload(0, 0, 0, 0, f0);
+
+    uint32_t kt = 0;
+    for (; kt + 2 * S - 1 <= nk; kt += S) {
+        static_for<S>([&](auto U) {
+            constexpr int u = decltype(U)::value;  // kt % 4 == 0: tile kt+u has slot (u/2)%2, parity u%2
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (u % 2 == 0) issue_a_pair((kt + u) / 2 + 1, ((u + 2) / 2) % 2);
+            fload((u / 2) % 2, u % 2, u, 1, f1);
+            mma(f0);
+            pin(std::integral_constant<int, u % 2 == 0 ? kPairLoads : 0>{});
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(u % 2 == 0 ? kLoadsB + kPairLoads : kLoadsB, 0));
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            issue_b(kt + u + 3, (u + 3) % S);
+            fload(((u + 1) / 2) % 2, (u + 1) % 2, (u + 1) % S, 0, f0);
+            mma(f1);
+            pin(std::integral_constant<int, kLoadsB>{});
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+    // Last iterations: requests only while tiles remain.
+    for (; kt < nk; kt++) {
+        const bool more = kt + 2 < nk;
+        if (kt % 2 == 0 && more) issue_a_pair(kt / 2 + 1, (kt / 2 + 1) % 2);
+        fload((kt / 2) % 2, kt % 2, kt % S, 1, f1);
+        mma(f0);
+        if (!more)
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+        else if (kt % 2 == 0)
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLoadsB + kPairLoads, 0));
+        else
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLoadsB, 0));
+        __builtin_amdgcn_s_barrier();
+        if (kt + 3 < nk) issue_b(kt + 3, (kt + 3) % S);
+        if (kt + 1 < nk) fload(((kt + 1) / 2) % 2, (kt + 1) % 2, (kt + 1) % S, 0, f0);
+        mma(f1);
+    }
+
+    if (m0 + BM <= M && n0 + BN <= N && p.ldc <= kFullEpiMaxLdc)
+        epilogue_tile_full<EPI, 4, FN, 4>(p, acc, m0 + wm * 128, n0 + wn * (BN / 2), lane);
+    else
+        epilogue_tile<EPI, 4, FN, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * (BN / 2) + lane % 32, M,
+                                     N);
+}
+
 // --------------------------- NT core GEMM, 8-wave ping-pong (2 waves/SIMD)
 
 namespace pp {
@@ -1396,6 +1610,13 @@ bool use_dma() {
     return !(env && env[0] == '0');
 }
 
+// A copied in k-step pairs (k_gemm_i8_dma_pairs) when K % 128 == 0, unless
+// RPLHIP_I8_PAIRS=0 (for A/B timing only).
+bool use_pairs(uint32_t K) {
+    static const char* env = getenv("RPLHIP_I8_PAIRS");
+    return K % (2 * dma::BK) == 0 && !(env && env[0] == '0');
+}
+
 template <class G, int EPI>
 int launch_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_t M, uint32_t N, uint32_t K,
               const EpiParams& p, bool al, hipStream_t s) {
@@ -1482,6 +1703,9 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
             if constexpr (RPL_I8_BIG_KERNEL == 1)
                 hipLaunchKernelGGL((k_gemm_i8_nt_pp<EPI>), dim3((uint32_t)tiles), dim3(pp::kThreads), 0, s, A, lda,
                                    B, ldb, M, N, K, p);
+            else if (use_pairs(K))
+                hipLaunchKernelGGL((k_gemm_i8_dma_pairs<EPI, false>), dim3((uint32_t)tiles), dim3(dma::kThreads), 0,
+                                   s, A, lda, B, ldb, M, N, K, p);
             else
                 hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256>), dim3((uint32_t)tiles), dim3(dma::kThreads), 0, s, A,
                                    lda, B, ldb, M, N, K, p);
@@ -1518,8 +1742,12 @@ template <int EPI>
 int launch_kn(const int8_t* A, const int8_t* B, uint32_t M, uint32_t N, uint32_t K, const EpiParams& p,
               hipStream_t s) {
     const uint32_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
-    hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256, true>), dim3(tiles), dim3(dma::kThreads), 0, s, A, K, B, N, M, N,
-                       K, p);
+    if (use_pairs(K))
+        hipLaunchKernelGGL((k_gemm_i8_dma_pairs<EPI, true>), dim3(tiles), dim3(dma::kThreads), 0, s, A, K, B, N, M,
+                           N, K, p);
+    else
+        hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256, true>), dim3(tiles), dim3(dma::kThreads), 0, s, A, K, B, N, M,
+                           N, K, p);
     return rplhip::check_launch("int8 GEMM ([K][N] B)");
 }
 

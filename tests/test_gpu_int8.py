@@ -230,7 +230,11 @@ def _requant_f32(acc, sa, sb, sc):
 # tile holds 48 columns and the chunks past them are clamped), and transpose
 # it first otherwise (5900, 3000).  (1800, 3000, 448) has too few 256 x 256
 # tiles and takes 256 x 128 ones (192 of them), with ragged M and N edges.
-BIG = [(5890, 5900, 832), (5890, 5888, 832), (6144, 6144, 448), (1800, 3000, 448), (2900, 4400, 448)]
+# K % 128 == 0 (896, 256, 128) copies A two k-steps at a time
+# (k_gemm_i8_dma_pairs): K = 896 runs its steady loop and a 6-tile tail,
+# K = 256 and 128 only the tail (4 and 2 tiles).
+BIG = [(5890, 5900, 832), (5890, 5888, 832), (6144, 6144, 448), (1800, 3000, 448), (2900, 4400, 448),
+       (5890, 5888, 896), (5890, 5900, 896), (2900, 4400, 256), (4096, 3072, 128)]
 
 
 @pytest.mark.parametrize("M,N,K", BIG)
