@@ -316,7 +316,7 @@ def main():
         tops = ops / (ms_i8 * 1e-3) / 1e12
 
     # Dominant kernel alone: gemm_int8 launches exactly one kernel
-    # (k_gemm_i8_nt_dma with B [K,N] read in place), timed on its stream.
+    # (k_gemm_i8_dma_pairs with B [K,N] read in place), timed on its stream.
     if want("int8-kernel") or args.only is None:
         log("bench: int8 GEMM kernel alone")
         ms_k, _ = timer.time(int8_step, args.steps, args.warmup)
