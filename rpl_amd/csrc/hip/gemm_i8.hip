@@ -1617,6 +1617,37 @@ bool use_pairs(uint32_t K) {
     return K % (2 * dma::BK) == 0 && !(env && env[0] == '0');
 }
 
+// The same epilogue over output columns n1..: the column-indexed inputs
+// (bias, B's column sums, per-column scales) and the output start n1 later.
+EpiParams shift_cols(EpiParams p, uint32_t n1) {
+    if (p.bias) p.bias += n1;
+    if (p.rowsum_b) p.rowsum_b += n1;
+    if (p.sw && p.sw_per_col) p.sw += n1;
+    if (p.out_i32) p.out_i32 += n1;
+    if (p.out_f32) p.out_f32 += n1;
+    return p;
+}
+
+// Rounds of 256 x 256 tiles (one block per CU) that end with a mostly idle
+// round: the columns of that round go to a second launch of 256 x 128
+// tiles, which run a round in ~0.76 of the big tile's time (2048 x 4096 x
+// 4096: 47 us for 256 of them against ~62 us per big round).  Returns the
+// width of the big-tile part (a multiple of 256), or 0 to keep one launch.
+// Config 3, 2048 x 11008: 344 tiles = 256 + 88 become 256 big tiles on
+// N = 8192 and 176 half tiles on the last 2816 columns.
+uint32_t balanced_split(uint32_t M, uint32_t N) {
+    static const char* env = getenv("RPLHIP_I8_SPLIT");
+    if (env && env[0] == '0') return 0;
+    const uint64_t C = rplhip::cu_count(), mt = (M + 255) / 256, T = mt * ((N + 255) / 256);
+    const uint64_t R = (T + C - 1) / C;
+    if (R < 2) return 0;
+    const uint64_t n1t = (R - 1) * C / mt;  // tile columns that fill R-1 rounds
+    if (n1t == 0 || 256 * n1t >= N) return 0;
+    const uint64_t r1 = (mt * n1t + C - 1) / C;
+    const uint64_t r2 = (mt * ((N - 256 * n1t + 127) / 128) + C - 1) / C;
+    return (double)r1 + 0.76 * (double)r2 < 0.95 * (double)R ? (uint32_t)(256 * n1t) : 0;
+}
+
 template <class G, int EPI>
 int launch_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_t M, uint32_t N, uint32_t K,
               const EpiParams& p, bool al, hipStream_t s) {
@@ -1698,6 +1729,21 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
         al && K % dma::BK == 0 && (uint64_t)M * lda < (1ull << 31) && (uint64_t)N * ldb < (1ull << 31) && use_dma();
     const uint64_t mt = (M + dma::BM - 1) / dma::BM;
     if (al && use_big_tile(M, N, dma_ok)) {
+        const uint32_t n1 = dma_ok && RPL_I8_BIG_KERNEL != 1 ? balanced_split(M, N) : 0;
+        if (n1) {
+            // Columns [0, n1) on big tiles, [n1, N) on 256 x 128 tiles.
+            const EpiParams p2 = shift_cols(p, n1);
+            const uint32_t tiles1 = (uint32_t)(mt * (n1 / 256)), tiles2 = (uint32_t)(mt * ((N - n1 + 127) / 128));
+            if (use_pairs(K))
+                hipLaunchKernelGGL((k_gemm_i8_dma_pairs<EPI, false>), dim3(tiles1), dim3(dma::kThreads), 0, s, A, lda,
+                                   B, ldb, M, n1, K, p);
+            else
+                hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256>), dim3(tiles1), dim3(dma::kThreads), 0, s, A, lda, B,
+                                   ldb, M, n1, K, p);
+            hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 128>), dim3(tiles2), dim3(dma::kThreads), 0, s, A, lda,
+                               B + (uint64_t)n1 * ldb, ldb, M, N - n1, K, p2);
+            return rplhip::check_launch("int8 GEMM (balanced halves)");
+        }
         if (dma_ok) {
             const uint64_t tiles = mt * ((N + 255) / 256);
             if constexpr (RPL_I8_BIG_KERNEL == 1)
