@@ -510,10 +510,11 @@ __device__ __forceinline__ void epilogue_tile_full(const EpiParams& p, const v16
 namespace dma {
 constexpr int BM = 256, BK = 64, S = RPL_I8_STAGES, kThreads = 256;
 // [K][N] B tiles: k-row r keeps its logical 16-byte chunk c in physical
-// chunk c ^ kn_swz(r % 8).  The XOR moves chunk bits 0, 1 and 3 and leaves
-// bit 2 alone, so fragments j and j+2 (columns 64 apart) stay 64 bytes apart
-// in every row and share one address register.
-__device__ __forceinline__ uint32_t kn_swz(uint32_t e) { return (e & 3) | ((e & 4) << 1); }
+// chunk c ^ kn_swz(r % 8).  Measured on gfx950 (SQ_LDS_BANK_CONFLICT per
+// ds_read_b64_tr_b8 of the fragment pattern): moving chunk bits 1-3 reads
+// without conflicts; any XOR that moves chunk bit 0 (the two 16-lane groups
+// reading adjacent chunks) costs 2 extra cycles per read.
+__device__ __forceinline__ uint32_t kn_swz(uint32_t e) { return 2 * e; }
 typedef __attribute__((address_space(3))) v2i* lds_v2i;
 // ds_read_b64_tr_b8 through a restrict parameter: inlining gives the read
 // alias-scope metadata, as the kernel's plain LDS reads have.  Without it
@@ -669,13 +670,12 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
     for (int kk = 0; kk < 2; kk++) foff[kk] = fr * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
     const uint32_t a_base = wm * 128 * BK, b_base = kTileBytesA + wn * (BN / 2) * BK;
     // [K][N] B: lane 16g + 2e + h reads k-row 16(g/2) + e (+ 32kk + 8t) at
-    // columns 128wn + 32j + 16(g%2) + 8h, in chunk
-    // (8wn + 2j + g%2) ^ kn_swz(e); fragments j and j+2 are 64 bytes apart.
-    uint32_t boff[2];
+    // columns 128wn + 32j + 16(g%2) + 8h, in chunk (8wn + 2j + g%2) ^ kn_swz(e).
+    uint32_t boff[4];
     if constexpr (BKN) {
         const uint32_t g = lane / 16, e = (lane % 16) / 2, h = lane % 2;
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 4; j++)
             boff[j] = kTileBytesA + (16 * (g / 2) + e) * 256 + ((8 * wn + 2 * j + g % 2) ^ dma::kn_swz(e)) * 16 + 8 * h;
     }
     using F = dma::Frags<FN>;
@@ -688,7 +688,7 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
             const int8_t* sb = smem + stage * kStageBytes + kk * 32 * 256;
 #pragma unroll
             for (int j = 0; j < FN; j++) {
-                const int8_t* pb = sb + boff[j % 2] + 64 * (j / 2);
+                const int8_t* pb = sb + boff[j];
                 const v2i lo = dma::tr8((lds_v2i)pb);
                 const v2i hi = dma::tr8((lds_v2i)(pb + 8 * 256));
                 f.b[j] = (v4i){lo.x, lo.y, hi.x, hi.y};
@@ -811,9 +811,10 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
 // half of 16 lines, and fetches each line twice).  A pair of A tiles fills a
 // 32 KB region laid out in 1 KB row groups: group g holds rows 8g..8g+7, the
 // first 512 bytes k-step 2p, the next 512 bytes k-step 2p+1, each as 8 rows
-// x 64 bytes with chunk c at slot c ^ swz(row % 8).  Lane l of a copy writes
-// bytes 16l..16l+15 of one group, so it fetches k-step l/32, row (l%32)/4,
-// chunk (l%4) ^ swz(row).  Fragment reads then see the per-k-step layout
+// x 64 bytes with chunk c at slot c ^ swz(row).  Lane l of a copy writes
+// bytes 16l..16l+15 of one group, so it fetches k-step l/32, row 8g +
+// (l%32)/4, chunk (l%4) ^ swz(row).  (Keying the swizzle on row % 8 alone
+// leaves rows 8 apart on the same banks: measured 4 extra cycles per read.)  Fragment reads then see the per-k-step layout
 // (64-byte rows, the same swizzle) at a parity offset of 0 or 512 bytes.
 //
 // LDS: two A pair regions (64 KB) and four B stages (64 KB).  Iteration j
@@ -853,8 +854,10 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_dma_pairs(const int8_t* __re
                                               : uniform_rsrc(B + (uint64_t)n0 * ldb, rows_b * ldb);
 
     // A pair copies: wave w fills row groups 8w .. 8w+7 (rows 64w .. 64w+63);
-    // copy i covers rows 64w + 8i + a_rr.  Rows past M are clamped to the
-    // last row (never stored).
+    // copy i covers rows R = 64w + 8i + a_rr.  The chunk swizzle is swz(R),
+    // with R % 32 = 8(i%4) + a_rr, so swz(R) = swz(a_rr) ^ 2(i%2): the
+    // column offset of copy i is a_col ^ 32(i%2).  Rows past M are clamped
+    // to the last row (never stored).
     const uint32_t a_rr = (lane % 32) / 4;
     const uint32_t a_row = wave * 64 + a_rr;
     const uint32_t a_col = (lane / 32) * BK + ((lane % 4) ^ swz(a_rr)) * 16;
@@ -864,8 +867,8 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_dma_pairs(const int8_t* __re
         for (int i = 0; i < kPairLoads; i++) {
             const uint32_t r = a_row + 8 * i;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr)(st + i * 1024), 16,
-                                                     (r < rows_a ? r : rows_a - 1) * lda + a_col, pair * 2 * BK, 0,
-                                                     0);
+                                                     (r < rows_a ? r : rows_a - 1) * lda + (a_col ^ (32 * (i % 2))),
+                                                     pair * 2 * BK, 0, 0);
         }
     };
     // B copies as in k_gemm_i8_nt_dma.
@@ -894,16 +897,16 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_dma_pairs(const int8_t* __re
     // Fragment reads.  A: row R = 128wm + 32i + fr lives in group R/8 at
     // row R%8 = fr%8.  B: as in k_gemm_i8_nt_dma.
     const uint32_t fr = lane % 32;
-    uint32_t foff_a[2], foff_b[2], boff[2];
+    uint32_t foff_a[2], foff_b[2], boff[4];
 #pragma unroll
     for (int kk = 0; kk < 2; kk++) {
-        foff_a[kk] = wm * 16 * 1024 + (fr / 8) * 1024 + (fr % 8) * BK + ((2 * kk + lane / 32) ^ swz(fr % 8)) * 16;
+        foff_a[kk] = wm * 16 * 1024 + (fr / 8) * 1024 + (fr % 8) * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
         if constexpr (!BKN) foff_b[kk] = wn * (BN / 2) * BK + fr * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
     }
     if constexpr (BKN) {
         const uint32_t g = lane / 16, e = (lane % 16) / 2, h = lane % 2;
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 4; j++)
             boff[j] = (16 * (g / 2) + e) * 256 + ((8 * wn + 2 * j + g % 2) ^ dma::kn_swz(e)) * 16 + 8 * h;
     }
     using F = dma::Frags<FN>;
@@ -917,7 +920,7 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_dma_pairs(const int8_t* __re
             const int8_t* sb = smem + kBBase + stage * kBStage + kk * 32 * 256;
 #pragma unroll
             for (int j = 0; j < FN; j++) {
-                const int8_t* pb = sb + boff[j % 2] + 64 * (j / 2);
+                const int8_t* pb = sb + boff[j];
                 const v2i lo = dma::tr8((lds_v2i)pb);
                 const v2i hi = dma::tr8((lds_v2i)(pb + 8 * 256));
                 f.b[j] = (v4i){lo.x, lo.y, hi.x, hi.y};

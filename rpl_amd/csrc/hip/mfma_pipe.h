@@ -19,11 +19,15 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // LDS tiles of 64-byte rows store the four 16-byte chunks of row r
-// XOR-swizzled (chunk c at slot c ^ swz(r)), so both the 128-bit fragment
-// reads (consecutive rows, same chunk) and the 128-bit tile writes (4 chunks
-// of consecutive rows) touch distinct banks whether the LDS serves 8 lanes x
-// 16 bytes over 32 banks or 16 lanes over 64 banks.
-__device__ __forceinline__ uint32_t swz(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// XOR-swizzled (chunk c at slot c ^ swz(r)).  The fragment reads have lane l
+// read row l%32 (plus a multiple of 32) at one chunk per half-wave; measured
+// on gfx950 (SQ_LDS_BANK_CONFLICT per ds_read_b128), this swizzle reads them
+// without bank conflicts, as do (r>>2)&3, (r>>3)&3 and (r^(r>>2))&3, while
+// ((r>>1)^(r>>3))&3 and (r>>1)&3 cost 4 extra cycles per read and no
+// swizzle 12.  The function must depend on r % 32 only (rows 32 apart share
+// lanes).  Tile writes fill whole 64-byte rows, which any row-local
+// permutation leaves conflict-free.
+__device__ __forceinline__ uint32_t swz(uint32_t r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 
 // Word 3 of a raw buffer resource on gfx950 (32-bit data format, no
 // swizzle, range-checked against num_records).
