@@ -441,6 +441,13 @@ __device__ __forceinline__ void epilogue_tile(const EpiParams& p, const v16i (&a
     });
 }
 
+// Cache policy of the full-tile epilogue's stores: 2 = non-temporal (the
+// output is written once and not read back by the GEMM).  Measured at
+// 8192^3 (gemm_int8): 0.4405 ms against 0.4476 with the default policy.
+#ifndef RPL_I8_EPI_CPOL
+#define RPL_I8_EPI_CPOL 2
+#endif
+
 // Largest ldc for which a 128-row wave sub-tile spans < 2^31 bytes of C.
 constexpr uint32_t kFullEpiMaxLdc = 1u << 21;
 
@@ -479,7 +486,7 @@ __device__ __forceinline__ void epilogue_tile_full(const EpiParams& p, const v16
             static_for<FN>([&](auto J) {
                 constexpr int j = decltype(J)::value;
                 const uint32_t bits = epi_bits<EPI>(p, acc[i][j][r], m, nb + j * 32, cadd[j], rmul, cmul[j]);
-                __builtin_amdgcn_raw_buffer_store_b32(bits, rsrc, (int)(voff + j * 128), soff, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(bits, rsrc, (int)(voff + j * 128), soff, RPL_I8_EPI_CPOL);
             });
         });
     });
