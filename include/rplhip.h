@@ -76,6 +76,17 @@ int rplhip_sgemm(int trans_a, int trans_b, uint32_t M, uint32_t N, uint32_t K, f
                  const float* A, uint32_t lda, const float* B, uint32_t ldb, float beta,
                  float* C, uint32_t ldc, rplhip_stream_t stream);
 
+/* `batch` GEMMs of one shape in one launch: C_z = alpha * op(A_z) * op(B_z)
+ * (+ beta * C_z when read_c), with X_z = X + z * stride_x (elements).
+ * read_c = 0 writes C without reading it (beta ignored).  No reference
+ * counterpart: it serves scaled_dot_product_attention
+ * (src/rpl_attention.c:30-107), whose per-batch tensor_gemm calls it
+ * replaces. */
+int rplhip_sgemm_batched(int trans_a, int trans_b, uint32_t M, uint32_t N, uint32_t K, float alpha,
+                         const float* A, uint32_t lda, uint64_t stride_a, const float* B, uint32_t ldb,
+                         uint64_t stride_b, float beta, float* C, uint32_t ldc, uint64_t stride_c,
+                         uint32_t batch, int read_c, rplhip_stream_t stream);
+
 /* ------------------------------------------------------------- INT8 GEMM */
 
 /* gemm_int8 (src/ops_extended.c:83-129): A [M,K] int8, B [K,N] int8,

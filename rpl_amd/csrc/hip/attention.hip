@@ -59,22 +59,36 @@ extern "C" int rplhip_attention(const float* Q, const float* K, const float* V, 
     int st = ws_alloc(&ws, n_scores * sizeof(float), s);
     if (st) return st;
     float* S = static_cast<float*>(ws);
-    // The GEMMs read C (beta = 0 still multiplies it): start from zeros.
-    st = rplhip_fill(S, n_scores, 0.0f, stream);
-    if (!st) st = rplhip_fill(out, (uint64_t)B * Sq * dv, 0.0f, stream);
     const float scale = 1.0f / sqrtf((float)dk);  // as the reference computes it
-    for (uint32_t b = 0; b < B && !st; b++)
-        st = rplhip_sgemm(0, 1, Sq, Sk, dk, scale, Q + (uint64_t)b * Sq * dk, dk, K + (uint64_t)b * Sk * dk, dk,
-                          0.0f, S + (uint64_t)b * Sq * Sk, Sk, stream);
+    // Per-batch score matrices big enough for the large-tile GEMM go one by
+    // one through rplhip_sgemm (which reads C: start from zeros); the rest
+    // take one batched launch per product that writes C without reading it.
+    const bool big = (uint64_t)((Sq + 255) / 256) * ((Sk + 255) / 256) >= 2ull * cu_count() && dk % 16 == 0;
+    if (big) {
+        st = rplhip_fill(S, n_scores, 0.0f, stream);
+        for (uint32_t b = 0; b < B && !st; b++)
+            st = rplhip_sgemm(0, 1, Sq, Sk, dk, scale, Q + (uint64_t)b * Sq * dk, dk, K + (uint64_t)b * Sk * dk, dk,
+                              0.0f, S + (uint64_t)b * Sq * Sk, Sk, stream);
+    } else {
+        st = rplhip_sgemm_batched(0, 1, Sq, Sk, dk, scale, Q, dk, (uint64_t)Sq * dk, K, dk, (uint64_t)Sk * dk, 0.0f,
+                                  S, Sk, (uint64_t)Sq * Sk, B, 0, stream);
+    }
     if (!st) {
         const uint64_t rows = (uint64_t)B * Sq;
         hipLaunchKernelGGL(k_masked_softmax, dim3((uint32_t)((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
                            dim3(64 * kRowsPerBlock), 0, s, S, mask, rows, Sk);
         st = check_launch("attention softmax");
     }
-    for (uint32_t b = 0; b < B && !st; b++)
-        st = rplhip_sgemm(0, 0, Sq, dv, Sk, 1.0f, S + (uint64_t)b * Sq * Sk, Sk, V + (uint64_t)b * Sk * dv, dv, 0.0f,
-                          out + (uint64_t)b * Sq * dv, dv, stream);
+    const bool big_pv = (uint64_t)((Sq + 255) / 256) * ((dv + 255) / 256) >= 2ull * cu_count() && Sk % 16 == 0;
+    if (big_pv) {
+        if (!st) st = rplhip_fill(out, (uint64_t)B * Sq * dv, 0.0f, stream);
+        for (uint32_t b = 0; b < B && !st; b++)
+            st = rplhip_sgemm(0, 0, Sq, dv, Sk, 1.0f, S + (uint64_t)b * Sq * Sk, Sk, V + (uint64_t)b * Sk * dv, dv,
+                              0.0f, out + (uint64_t)b * Sq * dv, dv, stream);
+    } else if (!st) {
+        st = rplhip_sgemm_batched(0, 0, Sq, dv, Sk, 1.0f, S, Sk, (uint64_t)Sq * Sk, V, dv, (uint64_t)Sk * dv, 0.0f,
+                                  out, dv, (uint64_t)Sq * dv, B, 0, stream);
+    }
     ws_free(ws, s);
     return st;
 }

@@ -129,12 +129,18 @@ struct Operand {
 // SPLIT: block (tile, blockIdx.y) multiplies only k in [blockIdx.y * kps,
 // +kps) (kps a multiple of BK) and stores the raw partial tile to
 // C + blockIdx.y * M * ldc (a workspace; alpha, beta are applied by
-// k_splitk_reduce).
+// k_splitk_reduce).  Batches: blockIdx.z selects matrices A + z*sA,
+// B + z*sB, C + z*sC.  read_c = 0 drops the read of C (beta is then
+// ignored); rplhip_sgemm always reads it, as the reference does.
 template <bool TA, bool TB, bool VEC, bool SPLIT>
 __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, uint32_t K, float alpha,
                                                        const float* __restrict__ A, uint32_t lda,
                                                        const float* __restrict__ B, uint32_t ldb, float beta,
-                                                       float* __restrict__ C, uint32_t ldc, uint32_t kps) {
+                                                       float* __restrict__ C, uint32_t ldc, uint32_t kps,
+                                                       uint64_t sA, uint64_t sB, uint64_t sC, int read_c) {
+    A += blockIdx.z * sA;
+    B += blockIdx.z * sB;
+    C += blockIdx.z * sC;
     using OpA = Operand<!TA, VEC>;
     using OpB = Operand<TB, VEC>;
     __shared__ __attribute__((aligned(16))) float As[2][kTileFloats];
@@ -221,7 +227,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, u
                 uint32_t n = n0 + wn + li * 4;
                 if (m >= M || n >= N) continue;
                 float4* cp = reinterpret_cast<float4*>(&C[(uint64_t)m * ldc + n]);
-                float4 c = *cp;
+                float4 c = read_c ? *cp : make_float4(0.f, 0.f, 0.f, 0.f);
                 c.x = alpha * acc[i][0][r] + beta * c.x;
                 c.y = alpha * acc[i][1][r] + beta * c.y;
                 c.z = alpha * acc[i][2][r] + beta * c.z;
@@ -239,7 +245,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, u
                     uint32_t n = n0 + OpB::row_of(wn, j, li);
                     if (m < M && n < N) {
                         float* cp = &C[(uint64_t)m * ldc + n];
-                        *cp = alpha * acc[i][j][r] + beta * *cp;
+                        *cp = alpha * acc[i][j][r] + (read_c ? beta * *cp : 0.0f);
                     }
                 }
     }
@@ -564,10 +570,10 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
         float* W = (float*)ws;
         if (vec)
             hipLaunchKernelGGL((k_sgemm<TA, TB, true, true>), g2, dim3(kThreads), 0, s, M, N, K, 1.0f, A, lda, B,
-                               ldb, 0.0f, W, N, kps);
+                               ldb, 0.0f, W, N, kps, 0ull, 0ull, 0ull, 1);
         else
             hipLaunchKernelGGL((k_sgemm<TA, TB, false, true>), g2, dim3(kThreads), 0, s, M, N, K, 1.0f, A, lda, B,
-                               ldb, 0.0f, W, N, kps);
+                               ldb, 0.0f, W, N, kps, 0ull, 0ull, 0ull, 1);
         st = rplhip::check_launch("sgemm (split-K)");
         if (!st) {
             const uint64_t total = (uint64_t)M * N;
@@ -580,11 +586,37 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
     }
     if (vec)
         hipLaunchKernelGGL((k_sgemm<TA, TB, true, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B,
-                           ldb, beta, C, ldc, K);
+                           ldb, beta, C, ldc, K, 0ull, 0ull, 0ull, 1);
     else
         hipLaunchKernelGGL((k_sgemm<TA, TB, false, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B,
-                           ldb, beta, C, ldc, K);
+                           ldb, beta, C, ldc, K, 0ull, 0ull, 0ull, 1);
     return rplhip::check_launch("sgemm");
+}
+
+// `batch` GEMMs of one shape in one launch of the 128 x 128 kernel (grid z =
+// batch index), C_z = alpha op(A_z) op(B_z) (+ beta C_z when read_c).
+template <bool TA, bool TB>
+int launch_batched(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint32_t lda, uint64_t sA,
+                   const float* B, uint32_t ldb, uint64_t sB, float beta, float* C, uint32_t ldc, uint64_t sC,
+                   uint32_t batch, int read_c, hipStream_t s) {
+    const bool vec = aligned16(A) && aligned16(B) && aligned16(C) && lda % 4 == 0 && ldb % 4 == 0 &&
+                     ldc % 4 == 0 && N % 4 == 0 && (TA ? M % 4 == 0 : K % 4 == 0) && (TB ? K % 4 == 0 : true) &&
+                     sA % 4 == 0 && sB % 4 == 0 && sC % 4 == 0;
+    const uint64_t tiles = (uint64_t)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
+    if (tiles > 0x7fffffffull) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "sgemm: %u x %u too large", M, N);
+    for (uint32_t b0 = 0; b0 < batch; b0 += 65535) {
+        const uint32_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
+        const dim3 grid((uint32_t)tiles, 1, nb);
+        if (vec)
+            hipLaunchKernelGGL((k_sgemm<TA, TB, true, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha,
+                               A + b0 * sA, lda, B + b0 * sB, ldb, beta, C + b0 * sC, ldc, K, sA, sB, sC, read_c);
+        else
+            hipLaunchKernelGGL((k_sgemm<TA, TB, false, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha,
+                               A + b0 * sA, lda, B + b0 * sB, ldb, beta, C + b0 * sC, ldc, K, sA, sB, sC, read_c);
+        const int st = rplhip::check_launch("sgemm (batched)");
+        if (st) return st;
+    }
+    return RPLHIP_OK;
 }
 
 }  // namespace
@@ -604,4 +636,27 @@ extern "C" int rplhip_sgemm(int trans_a, int trans_b, uint32_t M, uint32_t N, ui
     if (!trans_a && trans_b) return launch<false, true>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
     if (trans_a && !trans_b) return launch<true, false>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
     return launch<true, true>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
+}
+
+extern "C" int rplhip_sgemm_batched(int trans_a, int trans_b, uint32_t M, uint32_t N, uint32_t K, float alpha,
+                                    const float* A, uint32_t lda, uint64_t stride_a, const float* B, uint32_t ldb,
+                                    uint64_t stride_b, float beta, float* C, uint32_t ldc, uint64_t stride_c,
+                                    uint32_t batch, int read_c, rplhip_stream_t stream) {
+    if (M == 0 || N == 0 || batch == 0) return RPLHIP_OK;
+    if (!C || (K && (!A || !B))) return fail(RPLHIP_ERR_INVALID, "rplhip_sgemm_batched: NULL pointer");
+    if (ldc < N || (K && (lda < (trans_a ? M : K) || ldb < (trans_b ? K : N))))
+        return fail(RPLHIP_ERR_INVALID, "rplhip_sgemm_batched: leading dimension too small");
+    RPLHIP_REQUIRE_DEVICE();
+    hipStream_t s = as_stream(stream);
+    if (!trans_a && !trans_b)
+        return launch_batched<false, false>(M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
+                                            stride_c, batch, read_c, s);
+    if (!trans_a && trans_b)
+        return launch_batched<false, true>(M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
+                                           stride_c, batch, read_c, s);
+    if (trans_a && !trans_b)
+        return launch_batched<true, false>(M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
+                                           stride_c, batch, read_c, s);
+    return launch_batched<true, true>(M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc, stride_c,
+                                      batch, read_c, s);
 }

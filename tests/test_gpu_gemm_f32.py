@@ -278,3 +278,31 @@ def test_workspace_reuse_across_streams(gpu):
         assert np.max(np.abs(out - ref) / (np.abs(A) @ np.abs(B))) <= fp32_tol(K)
     for s in streams:
         check(lib.rplhip_stream_destroy(s), "stream_destroy")
+
+
+# rplhip_sgemm_batched: one launch for `batch` GEMMs of one shape (the
+# attention products).  read_c = 0 writes C without reading it (C starts as
+# NaN and none may survive); read_c = 1 is alpha*AB + beta*C per batch.
+@pytest.mark.parametrize("M,N,K,ta,tb,batch", [(64, 64, 32, 0, 1, 3), (200, 130, 48, 0, 0, 5), (33, 17, 9, 1, 0, 2),
+                                               (128, 256, 64, 1, 1, 7), (130, 72, 300, 0, 1, 1)])
+def test_sgemm_batched(gpu, M, N, K, ta, tb, batch):
+    from gpu_util import down, empty, up
+    lib = gpu
+    rng = np.random.default_rng(M + N + K + batch)
+    A = rng.uniform(-1, 1, (batch,) + ((K, M) if ta else (M, K))).astype(np.float32)
+    B = rng.uniform(-1, 1, (batch,) + ((N, K) if tb else (K, N))).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (batch, M, N)).astype(np.float32)
+    lda, ldb = (M if ta else K), (K if tb else N)
+    dA, dB = up(A), up(B)
+    for read_c in (0, 1):
+        dC = up(np.full((batch, M, N), np.nan, np.float32) if read_c == 0 else C0)
+        say("sgemm batched", M, N, K, ta, tb, batch, read_c)
+        rpl_amd.check(lib.rplhip_sgemm_batched(ta, tb, M, N, K, 1.25, dA.ptr, lda, M * K, dB.ptr, ldb, N * K, 0.5,
+                                               dC.ptr, N, M * N, batch, read_c, None))
+        got = down(dC, np.float32, (batch, M, N))
+        assert np.isfinite(got).all()
+        for z in range(batch):
+            a, b = op(A[z], ta), op(B[z], tb)
+            ref = 1.25 * (a.astype(np.float64) @ b.astype(np.float64)) + (0.5 * C0[z] if read_c else 0.0)
+            assert gemm_err_ratio(got[z], a, b, ref, 1.25, 0.5 if read_c else 0.0,
+                                  C0[z] if read_c else None) <= fp32_tol(K)
