@@ -524,9 +524,11 @@ __global__ void __launch_bounds__(256) k_splitk_reduce(const float* __restrict__
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
 // K splits for a grid of `tiles` tiles: enough blocks to fill the CUs twice,
-// each split at least kMinKSplit long (a multiple of BK); 1 = no split.
+// each split at least RPL_F32_MIN_KSPLIT long (a multiple of BK); 1 = no
+// split.  Measured minimum lengths 256 / 128 / 64: config 0 (512^3) 27.0 /
+// 19.2 / 17.3 us, config 2's MLP step 219 / 202 / 210 us.
 #ifndef RPL_F32_MIN_KSPLIT
-#define RPL_F32_MIN_KSPLIT 256
+#define RPL_F32_MIN_KSPLIT 128
 #endif
 uint32_t k_splits(uint64_t tiles, uint32_t K) {
     const uint64_t want = 2ull * rplhip::cu_count();
