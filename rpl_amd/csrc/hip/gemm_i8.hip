@@ -1313,7 +1313,9 @@ __global__ void __launch_bounds__(64 * WAVES) k_skinny(const int8_t* __restrict_
 #pragma unroll
             for (int q = 0; q < PANELS; q++)
                 wv[r][q][i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w_row(q, row) + k));
-            xv[r][i] = *reinterpret_cast<const v4i*>(a_row(row) + k);
+            // Row groups at or past M only feed output rows that are never
+            // stored: neither loaded nor written to LDS.
+            if (4 * i < (int)M) xv[r][i] = *reinterpret_cast<const v4i*>(a_row(row) + k);
         }
     };
 
@@ -1332,7 +1334,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_skinny(const int8_t* __restrict_
             const uint32_t row = 4 * i + wrow, off = row * kChunk + ((wchunk ^ row) * 16);
 #pragma unroll
             for (int q = 0; q < PANELS; q++) *reinterpret_cast<v4i*>(wbuf(q) + off) = wv[r][q][i];
-            *reinterpret_cast<v4i*>(xbuf + off) = xv[r][i];
+            if (4 * i < (int)M) *reinterpret_cast<v4i*>(xbuf + off) = xv[r][i];
         }
         if constexpr (st + kRegStages < kMaxStages) request(std::integral_constant<int, st + kRegStages>{});
         const uint32_t kb = kbeg + st * kChunk;
