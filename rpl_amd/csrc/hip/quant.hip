@@ -127,6 +127,53 @@ __global__ void __launch_bounds__(kThreads) k_quantize(const float* __restrict__
     for (uint64_t i = n4 * 4 + tid; i < n; i += stride) q[i] = quantize_one(x[i], scale, zp);
 }
 
+// Stage 2 and the quantization in one launch: every block combines the
+// (few) stage-1 partials itself, derives the parameters exactly as
+// k_min_max_finish<F> does (min / max selection is order-free, the formulas
+// are the same), block 0 stores them, and the block quantizes its share of
+// x as k_quantize does.
+template <int F>
+__global__ void __launch_bounds__(kThreads) k_quantize_chain(const float* __restrict__ x, uint64_t n,
+                                                             const float2* __restrict__ part, int nparts,
+                                                             float* __restrict__ out_f, int32_t* __restrict__ out_zp,
+                                                             int8_t* __restrict__ q) {
+    float mn = FLT_MAX, mx = -FLT_MAX;
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+        float2 p = part[i];
+        mn = sel_min(p.x, mn);
+        mx = sel_max(p.y, mx);
+    }
+    block_min_max(mn, mx);
+    float scale;
+    int32_t zp = 0;
+    if (F == kSymmetric) {
+        scale = fmaxf(fabsf(mn), fabsf(mx)) / 127.0f;
+    } else {
+        const float range = mx - mn;
+        scale = range / 255.0f;
+        zp = x86_cvt_i32(roundf(-mn / scale));
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        out_f[0] = scale;
+        if (F == kAsymmetric) out_zp[0] = zp;
+    }
+    uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    bool vec = ((((uintptr_t)x) & 15) == 0) && ((((uintptr_t)q) & 3) == 0);
+    uint64_t n4 = vec ? n / 4 : 0;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    uint32_t* q4 = reinterpret_cast<uint32_t*>(q);
+    for (uint64_t i = tid; i < n4; i += stride) {
+        float4 v = x4[i];
+        uint32_t b0 = (uint8_t)quantize_one(v.x, scale, zp);
+        uint32_t b1 = (uint8_t)quantize_one(v.y, scale, zp);
+        uint32_t b2 = (uint8_t)quantize_one(v.z, scale, zp);
+        uint32_t b3 = (uint8_t)quantize_one(v.w, scale, zp);
+        q4[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    }
+    for (uint64_t i = n4 * 4 + tid; i < n; i += stride) q[i] = quantize_one(x[i], scale, zp);
+}
+
 // y = (float)(q - zp) * scale  (ops_extended.c:69)
 __global__ void __launch_bounds__(kThreads) k_dequantize(const int8_t* __restrict__ q, uint64_t n,
                                                          float scale, int32_t zp,
@@ -290,6 +337,22 @@ int min_max_chain(const float* x, uint64_t n, float* out_f, int32_t* out_zp, hip
     return st;
 }
 
+// Symmetric / asymmetric quantization of x[0..n), n > 0: min/max partials,
+// then k_quantize_chain (two launches).
+template <int F>
+int quantize_chain(const float* x, uint64_t n, int8_t* q, float* out_f, int32_t* out_zp, hipStream_t s) {
+    int g = grid_for((n + 3) / 4);
+    void* ws = nullptr;
+    int st = rplhip::ws_alloc(&ws, sizeof(float2) * g, s);
+    if (st) return st;
+    hipLaunchKernelGGL(k_min_max_partial, dim3(g), dim3(kThreads), 0, s, x, n, (float2*)ws);
+    hipLaunchKernelGGL(k_quantize_chain<F>, dim3(g), dim3(kThreads), 0, s, x, n, (const float2*)ws, g, out_f,
+                       out_zp, q);
+    st = rplhip::check_launch("quantize");
+    rplhip::ws_free(ws, s);
+    return st;
+}
+
 }  // namespace
 
 using namespace rplhip;
@@ -318,11 +381,8 @@ int rplhip_quantize_symmetric(const float* x, uint64_t n, int8_t* q, float* scal
     if (!x || !q || !scale_out) return fail(RPLHIP_ERR_INVALID, "rplhip_quantize_symmetric: NULL pointer");
     RPLHIP_REQUIRE_DEVICE();
     hipStream_t s = as_stream(stream);
-    int st = min_max_chain<kSymmetric>(x, n, scale_out, nullptr, s);
-    if (st || n == 0) return st;
-    hipLaunchKernelGGL(k_quantize, dim3(grid_for((n + 3) / 4)), dim3(kThreads), 0, s, x, n, 0.0f, 0,
-                       (const float*)scale_out, (const int32_t*)nullptr, q);
-    return check_launch("quantize_symmetric");
+    if (n == 0) return min_max_chain<kSymmetric>(x, n, scale_out, nullptr, s);
+    return quantize_chain<kSymmetric>(x, n, q, scale_out, nullptr, s);
 }
 
 int rplhip_quantize_asymmetric(const float* x, uint64_t n, int8_t* q, float* scale_out,
@@ -331,11 +391,8 @@ int rplhip_quantize_asymmetric(const float* x, uint64_t n, int8_t* q, float* sca
         return fail(RPLHIP_ERR_INVALID, "rplhip_quantize_asymmetric: NULL pointer");
     RPLHIP_REQUIRE_DEVICE();
     hipStream_t s = as_stream(stream);
-    int st = min_max_chain<kAsymmetric>(x, n, scale_out, zp_out, s);
-    if (st || n == 0) return st;
-    hipLaunchKernelGGL(k_quantize, dim3(grid_for((n + 3) / 4)), dim3(kThreads), 0, s, x, n, 0.0f, 0,
-                       (const float*)scale_out, (const int32_t*)zp_out, q);
-    return check_launch("quantize_asymmetric");
+    if (n == 0) return min_max_chain<kAsymmetric>(x, n, scale_out, zp_out, s);
+    return quantize_chain<kAsymmetric>(x, n, q, scale_out, zp_out, s);
 }
 
 int rplhip_quantize_per_channel(const float* x, uint32_t num_channels, uint32_t channel_size,
