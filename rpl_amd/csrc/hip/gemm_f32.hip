@@ -353,7 +353,7 @@ template <bool TA, bool TB>
 __global__ void __launch_bounds__(256, 1) k_sgemm_dma(uint32_t M, uint32_t N, uint32_t K, float alpha,
                                                       const float* __restrict__ A, uint32_t lda,
                                                       const float* __restrict__ B, uint32_t ldb, float beta,
-                                                      float* __restrict__ C, uint32_t ldc) {
+                                                      float* __restrict__ C, uint32_t ldc, int read_c) {
     using fd::BK;
     using fd::BM;
     using fd::BN;
@@ -490,7 +490,7 @@ __global__ void __launch_bounds__(256, 1) k_sgemm_dma(uint32_t M, uint32_t N, ui
                 const uint32_t n = nw + 4 * (lane % 32);
                 if (full || n + 3 < N) {
                     float4* cp = reinterpret_cast<float4*>(crow + n);
-                    float4 c = *cp;
+                    float4 c = read_c ? *cp : make_float4(0.f, 0.f, 0.f, 0.f);
                     c.x = alpha * acc[i][0][r] + beta * c.x;
                     c.y = alpha * acc[i][1][r] + beta * c.y;
                     c.z = alpha * acc[i][2][r] + beta * c.z;
@@ -501,7 +501,7 @@ __global__ void __launch_bounds__(256, 1) k_sgemm_dma(uint32_t M, uint32_t N, ui
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const uint32_t n = nw + j * 32 + lane % 32;
-                    if (full || n < N) crow[n] = alpha * acc[i][j][r] + beta * crow[n];
+                    if (full || n < N) crow[n] = alpha * acc[i][j][r] + (read_c ? beta * crow[n] : 0.0f);
                 }
             }
         }
@@ -511,14 +511,14 @@ __global__ void __launch_bounds__(256, 1) k_sgemm_dma(uint32_t M, uint32_t N, ui
 // ld N), summed in split order (deterministic).
 __global__ void __launch_bounds__(256) k_splitk_reduce(const float* __restrict__ W, uint32_t splits, uint32_t M,
                                                        uint32_t N, float alpha, float beta, float* __restrict__ C,
-                                                       uint32_t ldc) {
+                                                       uint32_t ldc, int read_c) {
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (uint64_t)M * N) return;
     const uint32_t m = (uint32_t)(i / N), n = (uint32_t)(i % N);
     float sum = W[i];
     for (uint32_t s = 1; s < splits; s++) sum += W[(uint64_t)s * M * N + i];
     float* cp = &C[(uint64_t)m * ldc + n];
-    *cp = alpha * sum + beta * *cp;
+    *cp = alpha * sum + (read_c ? beta * *cp : 0.0f);
 }
 
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
@@ -538,9 +538,11 @@ uint32_t k_splits(uint64_t tiles, uint32_t K) {
     return (uint32_t)(s < cap ? s : cap);
 }
 
+// read_c = 0: C is written without being read (beta ignored); the result
+// equals that of read_c = 1 over C = 0 bit for bit (alpha*x + 0.0f).
 template <bool TA, bool TB>
 int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint32_t lda, const float* B,
-           uint32_t ldb, float beta, float* C, uint32_t ldc, hipStream_t s) {
+           uint32_t ldb, float beta, float* C, uint32_t ldc, hipStream_t s, int read_c = 1) {
     // 128-bit paths need the contiguous extents and leading dimensions to be
     // multiples of 4 floats and 16-byte aligned bases.
     bool vec = aligned16(A) && aligned16(B) && aligned16(C) && lda % 4 == 0 && ldb % 4 == 0 &&
@@ -556,7 +558,7 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
     if (vec && K >= fd::BK && K % fd::BK == 0 && big_tiles >= 2ull * rplhip::cu_count() && a_bytes < (1ull << 31) &&
         b_bytes < (1ull << 31) && !(dma_env && dma_env[0] == '0')) {
         hipLaunchKernelGGL((k_sgemm_dma<TA, TB>), dim3((uint32_t)big_tiles), dim3(fd::kThreads), 0, s, M, N, K, alpha,
-                           A, lda, B, ldb, beta, C, ldc);
+                           A, lda, B, ldb, beta, C, ldc, read_c);
         return rplhip::check_launch("sgemm (direct-to-LDS)");
     }
     const uint32_t splits = k_splits(tiles, K);
@@ -580,7 +582,7 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
         if (!st) {
             const uint64_t total = (uint64_t)M * N;
             hipLaunchKernelGGL(k_splitk_reduce, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, W, ns, M, N,
-                               alpha, beta, C, ldc);
+                               alpha, beta, C, ldc, read_c);
             st = rplhip::check_launch("sgemm (split-K reduction)");
         }
         rplhip::ws_free(ws, s);
@@ -588,10 +590,10 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
     }
     if (vec)
         hipLaunchKernelGGL((k_sgemm<TA, TB, true, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B,
-                           ldb, beta, C, ldc, K, 0ull, 0ull, 0ull, 1);
+                           ldb, beta, C, ldc, K, 0ull, 0ull, 0ull, read_c);
     else
         hipLaunchKernelGGL((k_sgemm<TA, TB, false, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B,
-                           ldb, beta, C, ldc, K, 0ull, 0ull, 0ull, 1);
+                           ldb, beta, C, ldc, K, 0ull, 0ull, 0ull, read_c);
     return rplhip::check_launch("sgemm");
 }
 
@@ -650,6 +652,12 @@ extern "C" int rplhip_sgemm_batched(int trans_a, int trans_b, uint32_t M, uint32
         return fail(RPLHIP_ERR_INVALID, "rplhip_sgemm_batched: leading dimension too small");
     RPLHIP_REQUIRE_DEVICE();
     hipStream_t s = as_stream(stream);
+    if (batch == 1) {  // one product: the full dispatch (large tiles, split-K)
+        if (!trans_a && !trans_b) return launch<false, false>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s, read_c);
+        if (!trans_a && trans_b) return launch<false, true>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s, read_c);
+        if (trans_a && !trans_b) return launch<true, false>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s, read_c);
+        return launch<true, true>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s, read_c);
+    }
     if (!trans_a && !trans_b)
         return launch_batched<false, false>(M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
                                             stride_c, batch, read_c, s);

@@ -284,13 +284,23 @@ Tensor* linear_forward(Linear* layer, const Tensor* input) {
     Tensor* matmul_out = create(2, output_shape, input->requires_grad || layer->weight->requires_grad);
     if (!matmul_out) return NULL;
     if (gpu && !rpl__attach(matmul_out, 0)) return NULL;
-    /* Zero the buffer the GEMM reads as C (beta = 0 still reads it): on the
-     * device only when resident (its host copy is stale by definition). */
-    if (gpu)
-        rpl__ok(rplhip_fill(rpl__dev_data(matmul_out), matmul_out->size, 0.0f, NULL), "linear_forward");
-    else
-        tensor_fill(matmul_out, 0.0f);
-    tensor_gemm(matmul_out, input, layer->weight, 1.0f, 0.0f, false, true);
+    /* The reference zeroes the buffer and runs tensor_gemm (beta = 0, which
+     * still reads C).  With input and weight resident, one GEMM that writes
+     * C without reading it gives the same bits (alpha*x + 0.0f) and skips
+     * the fill; otherwise zero the buffer (on the device when resident: its
+     * host copy is stale by definition) and go through tensor_gemm. */
+    const uint32_t M = input->shape[0], K = input->shape[1], N = layer->out_features;
+    if (gpu && rpl__is_gpu(input) && rpl__is_gpu(layer->weight) && input->dims == 2 && K == layer->in_features) {
+        rpl__ok(rplhip_sgemm_batched(0, 1, M, N, K, 1.0f, rpl__dev_data(input), K, 0, rpl__dev_data(layer->weight),
+                                     K, 0, 0.0f, rpl__dev_data(matmul_out), N, 0, 1, 0, NULL),
+                "linear_forward");
+    } else {
+        if (gpu)
+            rpl__ok(rplhip_fill(rpl__dev_data(matmul_out), matmul_out->size, 0.0f, NULL), "linear_forward");
+        else
+            tensor_fill(matmul_out, 0.0f);
+        tensor_gemm(matmul_out, input, layer->weight, 1.0f, 0.0f, false, true);
+    }
     if (matmul_out->requires_grad) {
         matmul_out->parent1 = (Tensor*)input;
         matmul_out->parent2 = layer->weight;
