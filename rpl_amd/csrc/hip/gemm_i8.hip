@@ -1245,10 +1245,10 @@ __global__ void __launch_bounds__(kSkThreads) k_gemv_i8_nt(const int8_t* __restr
 //
 // Block: PANELS 16-row panels of W (the N side of the MFMA), WAVES waves
 // splitting K into slices of at most kMaxSlice bytes; a wave walks its
-// slice in kMaxStages stages of 256 k-bytes with kRegStages stages in
-// flight, and reuses each A fragment for all PANELS panels (halving A's L2
-// traffic at PANELS = 2).  The partial tiles of the waves are summed through
-// LDS (int32, wrapping).  The code is straight-line (fully unrolled); loads
+// slice in kMaxStages stages of 256 k-bytes with RS stages in flight
+// (kRegStages with one panel, kTwoPanelStages with two), and reuses each A
+// fragment for all PANELS panels (halving A's L2 traffic at PANELS = 2).
+// The partial tiles of the waves are summed through LDS (int32, wrapping).  The code is straight-line (fully unrolled); loads
 // are ordinary, so the compiler's waits are exact, and slices shorter than
 // kMaxSlice load clamped (valid) addresses whose products are skipped.  A
 // wave's LDS writes and reads execute in order, so no barrier separates a
@@ -1260,22 +1260,28 @@ __global__ void __launch_bounds__(kSkThreads) k_gemv_i8_nt(const int8_t* __restr
 #ifndef RPL_SK_REG_STAGES
 #define RPL_SK_REG_STAGES 4
 #endif
+#ifndef RPL_SK_TWO_PANEL_STAGES
+#define RPL_SK_TWO_PANEL_STAGES 3  // M = 16, K = N = 8192: 12.3 us against 12.8 with 4 stages in flight
+#endif
 #ifndef RPL_SK_ONE_PANEL_MAX_M
 #define RPL_SK_ONE_PANEL_MAX_M 8  // larger M: two W panels per block share A (M = 16, K = N = 8192: 12.85 us against 13.24)
 #endif
 namespace sk {
 constexpr int kChunk = 256, kMaxSlice = 2048, kRegStages = RPL_SK_REG_STAGES;
+constexpr int kTwoPanelStages = RPL_SK_TWO_PANEL_STAGES;
 constexpr int kStageBytes = 16 * kChunk;  // one 16-row panel, one stage
 constexpr int kSteps = kChunk / 64;       // MFMA k-steps per stage
 constexpr int kMaxStages = kMaxSlice / kChunk;
 static_assert(kRegStages >= 1 && kRegStages <= kMaxStages, "stages in flight");
+static_assert(kTwoPanelStages >= 1 && kTwoPanelStages <= kMaxStages, "stages in flight");
 }  // namespace sk
 
-template <int EPI, int WAVES, int PANELS>
+template <int EPI, int WAVES, int PANELS, int RS = sk::kRegStages>
 __global__ void __launch_bounds__(64 * WAVES) k_skinny(const int8_t* __restrict__ A, uint32_t lda,
                                                        const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
                                                        uint32_t N, uint32_t K, uint32_t kpw, EpiParams p) {
     using namespace sk;
+    static_assert(RS >= 1 && RS <= kMaxStages, "stages in flight");
     // Per wave: one staging buffer for each W panel and one for A.  A
     // wave's LDS operations execute in issue order, so the next stage's
     // writes cannot overtake this stage's reads.
@@ -1302,9 +1308,9 @@ __global__ void __launch_bounds__(64 * WAVES) k_skinny(const int8_t* __restrict_
         return B + (uint64_t)(n < N ? n : N - 1) * ldb;
     };
     auto a_row = [&](uint32_t m) { return A + (uint64_t)(m < M ? m : M - 1) * lda; };
-    v4i wv[kRegStages][PANELS][4], xv[kRegStages][4];
+    v4i wv[RS][PANELS][4], xv[RS][4];
     auto request = [&](auto T) {
-        constexpr int st = decltype(T)::value, r = st % kRegStages;
+        constexpr int st = decltype(T)::value, r = st % RS;
         uint32_t k = kbeg + st * kChunk + wchunk * 16;
         k = k < kend ? k : kend - 16;  // past the slice: valid bytes, never multiplied
 #pragma unroll
@@ -1323,11 +1329,11 @@ __global__ void __launch_bounds__(64 * WAVES) k_skinny(const int8_t* __restrict_
 #pragma unroll
     for (int q = 0; q < PANELS; q++) acc[q] = (v4i){0, 0, 0, 0};
     const uint32_t fr = lane % 16;
-    static_for<kRegStages>([&](auto T) { request(T); });
+    static_for<RS>([&](auto T) { request(T); });
     static_for<kMaxStages>([&](auto T) {
-        constexpr int st = decltype(T)::value, r = st % kRegStages;
+        constexpr int st = decltype(T)::value, r = st % RS;
         // Stage st landed (the compiler waits for exactly these loads):
-        // write it into this stage's buffers, request stage st + kRegStages,
+        // write it into this stage's buffers, request stage st + RS,
         // then read the fragments back and multiply.
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -1336,7 +1342,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_skinny(const int8_t* __restrict_
             for (int q = 0; q < PANELS; q++) *reinterpret_cast<v4i*>(wbuf(q) + off) = wv[r][q][i];
             if (4 * i < (int)M) *reinterpret_cast<v4i*>(xbuf + off) = xv[r][i];
         }
-        if constexpr (st + kRegStages < kMaxStages) request(std::integral_constant<int, st + kRegStages>{});
+        if constexpr (st + RS < kMaxStages) request(std::integral_constant<int, st + RS>{});
         const uint32_t kb = kbeg + st * kChunk;
         const uint32_t left = kend > kb ? (kend - kb) / 64 : 0;
         v4i xs[kSteps];
@@ -1712,7 +1718,7 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
         const dim3 grid(two ? (N + 31) / 32 : (N + 15) / 16);
         if constexpr (RPL_SK_ONE_PANEL_MAX_M < 16) {  // two panels are only reachable below M = 16
             if (two) {
-                hipLaunchKernelGGL((k_skinny<EPI, 4, 2>), grid, dim3(256), 0, s, A, lda, B, ldb, M, N, K, kpw, p);
+                hipLaunchKernelGGL((k_skinny<EPI, 4, 2, sk::kTwoPanelStages>), grid, dim3(256), 0, s, A, lda, B, ldb, M, N, K, kpw, p);
                 return rplhip::check_launch("skinny int8 GEMM");
             }
         }
