@@ -1680,9 +1680,27 @@ int launch_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint
     return rplhip::check_launch("int8 GEMM");
 }
 
+// K = 0: every accumulator is the empty sum 0 (the k loops of
+// src/ops_extended.c:114 and src/rpl_quantization.c:335-345 run no
+// iteration), so only the epilogue runs (src/ops_extended.c:119-120, the bias
+// add at src/rpl_quantization.c:346-347) and no operand is read.  The GEMM
+// kernels' pipelines assume at least one k-step (the pairs kernel two).
+template <int EPI>
+__global__ void __launch_bounds__(256) k_epilogue_k0(uint32_t M, uint32_t N, EpiParams p) {
+    const uint64_t total = (uint64_t)M * N;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (uint64_t)gridDim.x * 256)
+        epilogue_store<EPI>(p, (uint32_t)(i / N), (uint32_t)(i % N), 0);
+}
+
 template <int EPI>
 int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_t M, uint32_t N, uint32_t K,
            const EpiParams& p, hipStream_t s) {
+    if (K == 0) {
+        const uint64_t blocks = ((uint64_t)M * N + 255) / 256;
+        hipLaunchKernelGGL((k_epilogue_k0<EPI>), dim3((uint32_t)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s,
+                           M, N, p);
+        return rplhip::check_launch("int8 GEMM, K = 0");
+    }
     bool al = K % 16 == 0 && lda % 16 == 0 && ldb % 16 == 0 && aligned16(A) && aligned16(B);
     const uint32_t Kp = (K + 1023) / 1024 * 1024;
     const bool skinny_ok = al && K >= 64 && K % 64 == 0 && K <= 8 * sk::kMaxSlice;

@@ -76,6 +76,33 @@ def test_linear_int8_vs_oracle(gpu, orc, M, K, N):
     assert bits_equal(linear_int8(x, w, None, M, K, N), orc.linear_int8(x, w, None, M, K, N))
 
 
+# K = 0: every accumulator is the empty sum, so the outputs are the epilogue
+# of 0 (requant of 0, sc = 0 -> 0/0 -> INT32_MIN, bias alone, 0 * scales).
+# 4096 x 4096 is a grid the big-tile kernels would otherwise take.
+@pytest.mark.parametrize("M,N", [(1, 7), (3, 5), (17, 40), (4096, 4096)])
+def test_int8_k0_vs_oracle(gpu, orc, M, N):
+    rng = np.random.default_rng(M + N)
+    A, B, W = np.zeros((M, 0), np.int8), np.zeros((0, N), np.int8), np.zeros((N, 0), np.int8)
+    for (sa, sb, sc, za, zb) in ((1.0, 1.0, 1.0, 0, 0), (0.013, 0.7, 0.29, -2, 9), (0.5, 0.25, 0.0, 0, 0),
+                                 (0.5, 0.25, 0.125, 0, 0)):
+        say("gemm_int8 K=0", M, N, sa, sb, sc, za, zb)
+        assert bits_equal(gemm_int8(A, B, M, N, 0, sa, sb, sc, za, zb), orc.gemm_int8(A, B, M, N, 0, sa, sb, sc, za, zb))
+    bias = rng.integers(-128, 128, N, dtype=np.int8)
+    for b in (bias, None):
+        say("linear_int8 K=0", M, N, b is not None)
+        assert bits_equal(linear_int8(A, W, b, M, 0, N), orc.linear_int8(A, W, b, M, 0, N))
+    sx = rng.random(M).astype(np.float32) * 0.01
+    sw = rng.random(N).astype(np.float32) * 0.02
+    say("linear_int8_dequant K=0", M, N)
+    want = orc.dequant_acc(np.zeros((M, N), np.int32), sx, True, sw, True)
+    assert bits_equal(linear_int8_dequant(A, sx, True, W, sw, True, M, 0, N), want)
+    lib = rpl_amd.lib()
+    dA, dB, dsa, dsb, dY = up(A), up(B), up(sx), up(sw), empty((M, N), np.float32)
+    say("gemm_int8_dequant K=0", M, N)
+    rpl_amd.check(lib.rplhip_gemm_int8_dequant(dA.ptr, dsa.ptr, 1, dB.ptr, dsb.ptr, 1, dY.ptr, M, N, 0, None))
+    assert bits_equal(down(dY, np.float32, (M, N)), want)
+
+
 @pytest.mark.parametrize("M,K,N", [(1, 256, 48), (16, 4096, 130), (77, 320, 200)])
 def test_linear_int8_dequant_vs_oracle(gpu, orc, M, K, N):
     rng = np.random.default_rng(K)
