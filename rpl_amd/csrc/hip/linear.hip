@@ -89,13 +89,33 @@ __global__ void __launch_bounds__(kThreads) k_colsum_partial(const float* __rest
     }
 }
 
-// Stage 2: db[c] += sum over splits (rpl_core.c:333).
+// Stage 2: db[c] += sum over splits (rpl_core.c:333).  Block = 64 columns x
+// 4 row lanes; lane r sums splits r, r+4, ... with 4 independent loads in
+// flight (a chain of one load per split was latency-bound: 11.6 us for 64
+// splits), then the lane sums are added in lane order (deterministic).
 __global__ void __launch_bounds__(kThreads) k_colsum_finish(const float* __restrict__ part, int splits,
                                                             uint64_t nb, float* __restrict__ db) {
-    GRID_STRIDE(c, nb) {
-        float s = 0;
-        for (int k = 0; k < splits; k++) s += part[(uint64_t)k * nb + c];
-        db[c] += s;
+    __shared__ float red[kRowLanes][kColTile];
+    const uint64_t c = (uint64_t)blockIdx.x * kColTile + threadIdx.x % kColTile;
+    const int lane_r = threadIdx.x / kColTile;
+    float s = 0;
+    if (c < nb) {
+        int k = lane_r;
+        for (; k + 3 * kRowLanes < splits; k += 4 * kRowLanes) {
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = part[(uint64_t)(k + j * kRowLanes) * nb + c];
+#pragma unroll
+            for (int j = 0; j < 4; j++) s += v[j];
+        }
+        for (; k < splits; k += kRowLanes) s += part[(uint64_t)k * nb + c];
+    }
+    red[lane_r][threadIdx.x % kColTile] = s;
+    __syncthreads();
+    if (lane_r == 0 && c < nb) {
+        float t = red[0][threadIdx.x];
+        for (int r = 1; r < kRowLanes; r++) t += red[r][threadIdx.x];
+        db[c] += t;
     }
 }
 
@@ -283,8 +303,8 @@ int rplhip_bias_grad(const float* dy, uint64_t n, float* db, uint64_t nb, rplhip
     // handled by the r*nb + c < n bound in the partial kernel.
     hipLaunchKernelGGL(k_colsum_partial, dim3((unsigned)cx, (unsigned)splits), dim3(kThreads), 0, s, dy, n,
                        full_rows, nb, rps, (float*)ws);
-    hipLaunchKernelGGL(k_colsum_finish, dim3(grid_for(nb)), dim3(kThreads), 0, s, (const float*)ws,
-                       (int)splits, nb, db);
+    hipLaunchKernelGGL(k_colsum_finish, dim3((unsigned)cx), dim3(kThreads), 0, s, (const float*)ws, (int)splits, nb,
+                       db);
     st = check_launch("bias_grad");
     ws_free(ws, s);
     return st;

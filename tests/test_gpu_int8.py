@@ -260,8 +260,10 @@ def _requant_f32(acc, sa, sb, sc):
 # K % 128 == 0 (896, 256, 128) copies A two k-steps at a time
 # (k_gemm_i8_dma_pairs): K = 896 runs its steady loop and a 6-tile tail,
 # K = 256 and 128 only the tail (4 and 2 tiles).
+# (4096, 3072, 128) is one k-step pair on the pairs kernel, (4096, 4096, 64)
+# a single k-step on the per-k-step kernel.
 BIG = [(5890, 5900, 832), (5890, 5888, 832), (6144, 6144, 448), (1800, 3000, 448), (2900, 4400, 448),
-       (5890, 5888, 896), (5890, 5900, 896), (2900, 4400, 256), (4096, 3072, 128)]
+       (5890, 5888, 896), (5890, 5900, 896), (2900, 4400, 256), (4096, 3072, 128), (4096, 4096, 64)]
 
 
 @pytest.mark.parametrize("M,N,K", BIG)
