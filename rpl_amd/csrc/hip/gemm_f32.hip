@@ -218,7 +218,20 @@ __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, u
                 }
     } else if (!TB && VEC) {
         // Interleaved columns: block j holds column li*4 + j -> 4 consecutive
-        // columns per lane, one float4 read-modify-write per (i, r).
+        // columns per lane, one float4 read-modify-write per (i, r).  All of
+        // the lane's C reads are issued before its first store: with a store
+        // between them the compiler cannot prove the next read's address
+        // different (it does not know ldc >= N, which the entry points
+        // check), so each read would wait for the one before (16 round trips).
+        float4 cv[FM][4];
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t m = m0 + OpA::row_of(wm, i, rg + r), n = n0 + wn + li * 4;
+                cv[i][r] = read_c && m < M && n < N ? *reinterpret_cast<const float4*>(&C[(uint64_t)m * ldc + n])
+                                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -226,15 +239,26 @@ __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, u
                 uint32_t m = m0 + OpA::row_of(wm, i, rg + r);
                 uint32_t n = n0 + wn + li * 4;
                 if (m >= M || n >= N) continue;
-                float4* cp = reinterpret_cast<float4*>(&C[(uint64_t)m * ldc + n]);
-                float4 c = read_c ? *cp : make_float4(0.f, 0.f, 0.f, 0.f);
+                float4 c = cv[i][r];
                 c.x = alpha * acc[i][0][r] + beta * c.x;
                 c.y = alpha * acc[i][1][r] + beta * c.y;
                 c.z = alpha * acc[i][2][r] + beta * c.z;
                 c.w = alpha * acc[i][3][r] + beta * c.w;
-                *cp = c;
+                *reinterpret_cast<float4*>(&C[(uint64_t)m * ldc + n]) = c;
             }
     } else {
+        // C reads first, then the stores (as above; 64 round trips per lane
+        // otherwise).
+        float cv[FM][FN][4];
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t m = m0 + OpA::row_of(wm, i, rg + r), n = n0 + OpB::row_of(wn, j, li);
+                    cv[i][j][r] = read_c && m < M && n < N ? C[(uint64_t)m * ldc + n] : 0.0f;
+                }
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -243,10 +267,8 @@ __global__ void __launch_bounds__(kThreads, 2) k_sgemm(uint32_t M, uint32_t N, u
                 for (int r = 0; r < 4; r++) {
                     uint32_t m = m0 + OpA::row_of(wm, i, rg + r);
                     uint32_t n = n0 + OpB::row_of(wn, j, li);
-                    if (m < M && n < N) {
-                        float* cp = &C[(uint64_t)m * ldc + n];
-                        *cp = alpha * acc[i][j][r] + (read_c ? beta * *cp : 0.0f);
-                    }
+                    if (m < M && n < N)
+                        C[(uint64_t)m * ldc + n] = alpha * acc[i][j][r] + (read_c ? beta * cv[i][j][r] : 0.0f);
                 }
     }
 }
@@ -476,35 +498,66 @@ __global__ void __launch_bounds__(256, 1) k_sgemm_dma(uint32_t M, uint32_t N, ui
 
     // Epilogue.  Result register r of lane l in block (i, j) is block-local
     // row 8(r/4) + 4(l/32) + r%4 and column l%32.
+    // Per row block i, all C reads are issued before the first store: with a
+    // store between two reads the compiler cannot prove the second address
+    // different (ldc >= N is checked by the entry points, not known here) and
+    // each read would wait for the one before (64 round trips per lane).
     const uint32_t mw = m0 + wm * 128, nw = n0 + wn * 128;
     const bool full = m0 + BM <= M && n0 + BN <= N;
+    auto row_m = [&](int i, int r) { return mw + OpA::row(i, 8 * (r / 4) + 4 * (lane / 32) + r % 4); };
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++) {
+        if (!TB) {
+            // Interleaved columns: block j holds column 4(l%32) + j.
+            const uint32_t n = nw + 4 * (lane % 32);
+            float4 cv[16];
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const uint32_t m = mw + OpA::row(i, 8 * (r / 4) + 4 * (lane / 32) + r % 4);
-            if (!full && m >= M) continue;
-            float* crow = C + (uint64_t)m * ldc;
-            if (!TB) {
-                // Interleaved columns: block j holds column 4(l%32) + j.
-                const uint32_t n = nw + 4 * (lane % 32);
-                if (full || n + 3 < N) {
-                    float4* cp = reinterpret_cast<float4*>(crow + n);
-                    float4 c = read_c ? *cp : make_float4(0.f, 0.f, 0.f, 0.f);
-                    c.x = alpha * acc[i][0][r] + beta * c.x;
-                    c.y = alpha * acc[i][1][r] + beta * c.y;
-                    c.z = alpha * acc[i][2][r] + beta * c.z;
-                    c.w = alpha * acc[i][3][r] + beta * c.w;
-                    *cp = c;
+            for (int r = 0; r < 16; r++) {
+                const uint32_t m = row_m(i, r);
+                const bool ok = full || (m < M && n + 3 < N);
+                cv[r] = read_c && ok ? *reinterpret_cast<const float4*>(C + (uint64_t)m * ldc + n)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t m = row_m(i, r);
+                if (!(full || (m < M && n + 3 < N))) continue;
+                float4 c = cv[r];
+                c.x = alpha * acc[i][0][r] + beta * c.x;
+                c.y = alpha * acc[i][1][r] + beta * c.y;
+                c.z = alpha * acc[i][2][r] + beta * c.z;
+                c.w = alpha * acc[i][3][r] + beta * c.w;
+                *reinterpret_cast<float4*>(C + (uint64_t)m * ldc + n) = c;
+            }
+        } else {
+            // Two halves of 8 rows, 32 reads in flight each (all 64 at once
+            // spilled scalar registers).
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                float cv[8][4];
+#pragma unroll
+                for (int r = 0; r < 8; r++) {
+                    const uint32_t m = row_m(i, 8 * h + r);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const uint32_t n = nw + j * 32 + lane % 32;
+                        cv[r][j] = read_c && (full || (m < M && n < N)) ? C[(uint64_t)m * ldc + n] : 0.0f;
+                    }
                 }
-            } else {
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const uint32_t n = nw + j * 32 + lane % 32;
-                    if (full || n < N) crow[n] = alpha * acc[i][j][r] + (read_c ? beta * crow[n] : 0.0f);
+                for (int r = 0; r < 8; r++) {
+                    const uint32_t m = row_m(i, 8 * h + r);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const uint32_t n = nw + j * 32 + lane % 32;
+                        if (full || (m < M && n < N))
+                            C[(uint64_t)m * ldc + n] =
+                                alpha * acc[i][j][8 * h + r] + (read_c ? beta * cv[r][j] : 0.0f);
+                    }
                 }
             }
         }
+    }
 }
 
 // C = alpha * sum_s W[s] + beta * C over the split partials W[s] ([M, N],
@@ -515,8 +568,19 @@ __global__ void __launch_bounds__(256) k_splitk_reduce(const float* __restrict__
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (uint64_t)M * N) return;
     const uint32_t m = (uint32_t)(i / N), n = (uint32_t)(i % N);
+    // Loads in batches of 8 (one chain of dependent loads was latency-bound:
+    // ~9 us for 32 splits); the additions keep split order.
+    const uint64_t stride = (uint64_t)M * N;
     float sum = W[i];
-    for (uint32_t s = 1; s < splits; s++) sum += W[(uint64_t)s * M * N + i];
+    uint32_t s = 1;
+    for (; s + 8 <= splits; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = W[(uint64_t)(s + j) * stride + i];
+#pragma unroll
+        for (int j = 0; j < 8; j++) sum += v[j];
+    }
+    for (; s < splits; s++) sum += W[(uint64_t)s * stride + i];
     float* cp = &C[(uint64_t)m * ldc + n];
     *cp = alpha * sum + (read_c ? beta * *cp : 0.0f);
 }
