@@ -602,6 +602,34 @@ uint32_t k_splits(uint64_t tiles, uint32_t K) {
     return (uint32_t)(s < cap ? s : cap);
 }
 
+// Small products (K <= 256, M*N*K <= 2^23; the MLP's 4096 x 128 x 10 and
+// 4096 x 10 x 128): one thread per output element on the VALU.  The 128 x 128
+// MFMA tile gives them 32 blocks, which leave most CUs idle (~18 us each).
+// The operation order is src/rpl_core.c:208-213's: sum = fma(a, b, sum) over
+// k in order, then C = fma(alpha, sum, beta * C) (GCC's contraction of
+// alpha*sum + beta*C), so these outputs equal the reference's bit for bit.
+template <bool TA, bool TB>
+__global__ void __launch_bounds__(256) k_sgemm_valu(uint32_t M, uint32_t N, uint32_t K, float alpha,
+                                                    const float* __restrict__ A, uint32_t lda,
+                                                    const float* __restrict__ B, uint32_t ldb, float beta,
+                                                    float* __restrict__ C, uint32_t ldc, int read_c) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (uint64_t)M * N) return;
+    const uint32_t m = (uint32_t)(i / N), n = (uint32_t)(i % N);
+    float sum = 0.0f;
+#pragma unroll 8
+    for (uint32_t k = 0; k < K; k++) {
+        const float a = TA ? A[(uint64_t)k * lda + m] : A[(uint64_t)m * lda + k];
+        const float b = TB ? B[(uint64_t)n * ldb + k] : B[(uint64_t)k * ldb + n];
+        sum = __builtin_fmaf(a, b, sum);
+    }
+    float* cp = &C[(uint64_t)m * ldc + n];
+    *cp = __builtin_fmaf(alpha, sum, read_c ? beta * *cp : 0.0f);
+}
+
+constexpr uint32_t kValuMaxK = 256;
+constexpr uint64_t kValuMaxWork = 1ull << 23;
+
 // read_c = 0: C is written without being read (beta ignored); the result
 // equals that of read_c = 1 over C = 0 bit for bit (alpha*x + 0.0f).
 template <bool TA, bool TB>
@@ -613,6 +641,12 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
                ldc % 4 == 0 && N % 4 == 0 && (TA ? M % 4 == 0 : K % 4 == 0) && (TB ? K % 4 == 0 : true);
     const uint64_t tiles = (uint64_t)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
     if (tiles > 0x7fffffffull) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "sgemm: %u x %u too large", M, N);
+    if (K > 0 && K <= kValuMaxK && (uint64_t)M * N * K <= kValuMaxWork) {
+        const uint64_t blocks = ((uint64_t)M * N + 255) / 256;  // M*N <= 2^23
+        hipLaunchKernelGGL((k_sgemm_valu<TA, TB>), dim3((uint32_t)blocks), dim3(256), 0, s, M, N, K, alpha, A, lda, B,
+                           ldb, beta, C, ldc, read_c);
+        return rplhip::check_launch("sgemm (VALU)");
+    }
     dim3 grid((uint32_t)tiles);
     // Big grids on the direct-to-LDS kernel (RPLHIP_F32_DMA=0 disables it,
     // for A/B timing only).

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import rpl_amd
-from conftest import seed
+from conftest import bits_equal, seed
 from gpu_util import fp32_tol, gemm_err_ratio, say, sgemm
 
 pytestmark = pytest.mark.gpu
@@ -27,6 +27,37 @@ def test_sgemm_golden(gpu, golden, name, ta, tb):
     say("sgemm golden", name, M, N, K)
     out = sgemm(A, B, C0, M, N, K, 0.75, -0.5, ta, tb)
     assert gemm_err_ratio(out, op(A, ta), op(B, tb), golden[f"sgemm_{name}_C"], 0.75, -0.5, C0) <= fp32_tol(K)
+
+
+# Products with K <= 256 and M*N*K <= 2^23 run on the VALU kernel in the
+# reference's operation order (sequential fma over k, then
+# fma(alpha, sum, beta*C)): bit-exact with the reference's golden vectors and
+# the oracle, including the MLP's 4096x128x10 and 4096x10x128.
+@pytest.mark.parametrize("name,ta,tb", [("nn", 0, 0), ("nt", 0, 1), ("tn", 1, 0), ("tt", 1, 1)])
+def test_sgemm_small_golden_bit_exact(gpu, golden, name, ta, tb):
+    A, B, C0 = golden[f"sgemm_{name}_A"], golden[f"sgemm_{name}_B"], golden[f"sgemm_{name}_C0"]
+    M, N = C0.shape
+    K = A.shape[0] if ta else A.shape[1]
+    say("sgemm small golden bit-exact", name, M, N, K)
+    assert bits_equal(sgemm(A, B, C0, M, N, K, 0.75, -0.5, ta, tb), golden[f"sgemm_{name}_C"])
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 128, 10), (4096, 10, 128), (1, 1, 1), (3, 5, 7), (33, 17, 256),
+                                   (200, 130, 1), (10, 128, 300)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_small_vs_oracle(gpu, orc, M, N, K, ta, tb):
+    rng = np.random.default_rng(M * 3 + N * 5 + K + 2 * ta + tb)
+    A = rng.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (N, K) if tb else (K, N)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+    for alpha, beta in ((1.0, 0.0), (0.75, -0.5), (1.0, 1.0)):
+        say("sgemm small", M, N, K, ta, tb, alpha, beta)
+        out = sgemm(A, B, C0, M, N, K, alpha, beta, ta, tb)
+        ref = orc.sgemm(A, B, C0, M, N, K, alpha, beta, bool(ta), bool(tb))
+        if K <= 256:
+            assert bits_equal(out, ref)
+        else:  # (10, 128, 300): past the VALU bound, on the MFMA tiles
+            assert gemm_err_ratio(out, op(A, ta), op(B, tb), ref, alpha, beta, C0) <= fp32_tol(K)
 
 
 def test_sgemm_nan_in_c_propagates(gpu, golden):
