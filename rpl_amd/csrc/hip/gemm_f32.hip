@@ -630,6 +630,30 @@ __global__ void __launch_bounds__(256) k_sgemm_valu(uint32_t M, uint32_t N, uint
 constexpr uint32_t kValuMaxK = 256;
 constexpr uint64_t kValuMaxWork = 1ull << 23;
 
+// The same products with a longer K (the MLP's dW2, 10 x 128 x 4096): block
+// row y sums k in [y * kps, +kps) into the workspace W[y] ([M, N], ld N), and
+// k_splitk_reduce adds the slices in order.  (The VALU path does two loads per
+// fma, so it stays within kValuMaxWork; larger products keep the MFMA tiles.)
+constexpr uint32_t kValuSlice = 64, kValuMaxSlices = 256;
+template <bool TA, bool TB>
+__global__ void __launch_bounds__(256) k_sgemm_valu_split(uint32_t M, uint32_t N, uint32_t K,
+                                                          const float* __restrict__ A, uint32_t lda,
+                                                          const float* __restrict__ B, uint32_t ldb,
+                                                          float* __restrict__ W, uint32_t kps) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (uint64_t)M * N) return;
+    const uint32_t m = (uint32_t)(i / N), n = (uint32_t)(i % N);
+    const uint32_t k0 = blockIdx.y * kps, k1 = k0 + kps < K ? k0 + kps : K;
+    float sum = 0.0f;
+#pragma unroll 8
+    for (uint32_t k = k0; k < k1; k++) {
+        const float a = TA ? A[(uint64_t)k * lda + m] : A[(uint64_t)m * lda + k];
+        const float b = TB ? B[(uint64_t)n * ldb + k] : B[(uint64_t)k * ldb + n];
+        sum = __builtin_fmaf(a, b, sum);
+    }
+    W[(uint64_t)blockIdx.y * M * N + i] = sum;
+}
+
 // read_c = 0: C is written without being read (beta ignored); the result
 // equals that of read_c = 1 over C = 0 bit for bit (alpha*x + 0.0f).
 template <bool TA, bool TB>
@@ -646,6 +670,26 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
         hipLaunchKernelGGL((k_sgemm_valu<TA, TB>), dim3((uint32_t)blocks), dim3(256), 0, s, M, N, K, alpha, A, lda, B,
                            ldb, beta, C, ldc, read_c);
         return rplhip::check_launch("sgemm (VALU)");
+    }
+    if (K > kValuMaxK && (uint64_t)M * N * K <= kValuMaxWork) {
+        uint32_t ns = (K + kValuSlice - 1) / kValuSlice;
+        if (ns > kValuMaxSlices) ns = kValuMaxSlices;
+        const uint32_t kps = (K + ns - 1) / ns;
+        ns = (K + kps - 1) / kps;
+        const uint32_t blocks = (uint32_t)(((uint64_t)M * N + 255) / 256);  // M*N <= 2^23 / 256
+        void* ws = nullptr;
+        int st = rplhip::ws_alloc(&ws, (size_t)ns * M * N * sizeof(float), s);
+        if (st) return st;
+        hipLaunchKernelGGL((k_sgemm_valu_split<TA, TB>), dim3(blocks, ns), dim3(256), 0, s, M, N, K, A, lda, B, ldb,
+                           (float*)ws, kps);
+        st = rplhip::check_launch("sgemm (VALU split-K)");
+        if (!st) {
+            hipLaunchKernelGGL(k_splitk_reduce, dim3(blocks), dim3(256), 0, s, (const float*)ws, ns, M, N, alpha, beta,
+                               C, ldc, read_c);
+            st = rplhip::check_launch("sgemm (VALU split-K reduction)");
+        }
+        rplhip::ws_free(ws, s);
+        return st;
     }
     dim3 grid((uint32_t)tiles);
     // Big grids on the direct-to-LDS kernel (RPLHIP_F32_DMA=0 disables it,

@@ -56,7 +56,7 @@ def test_sgemm_small_vs_oracle(gpu, orc, M, N, K, ta, tb):
         ref = orc.sgemm(A, B, C0, M, N, K, alpha, beta, bool(ta), bool(tb))
         if K <= 256:
             assert bits_equal(out, ref)
-        else:  # (10, 128, 300): past the VALU bound, on the MFMA tiles
+        else:  # (10, 128, 300): K past the single-pass bound, summed in k slices (VALU split-K)
             assert gemm_err_ratio(out, op(A, ta), op(B, tb), ref, alpha, beta, C0) <= fp32_tol(K)
 
 
