@@ -71,15 +71,34 @@ class Timer:
         return ms.value / steps, wall
 
 
-def cpu_baseline_int8(n, rows, qa, qb):
-    """The oracle (reference CPU path restated, same flags) on a row slab."""
-    from oracle import Oracle
+REF_LIB = os.path.join(REPO, "oracle", "_ref", "libref.so")
 
-    orc = Oracle()
-    t0 = time.perf_counter()
-    orc.gemm_int8(qa[:rows], qb, rows, n, n, rows=None)
+
+def cpu_baseline_int8(n, rows, qa, qb):
+    """The reference's own CPU gemm_int8 (src/ops_extended.c:124-129 ->
+    gemm_int8_fallback :83-122, OpenMP over output elements), compiled from
+    the reference sources into oracle/_ref/libref.so by oracle/Makefile, on a
+    row slab of the same inputs; the oracle's restatement (same loop, same
+    flags) when that build is absent.  Returns (TOP/s, seconds, kind)."""
+    a = np.ascontiguousarray(qa[:rows])
+    b = np.ascontiguousarray(qb)
+    out = np.empty((rows, n), np.int32)
+    if os.path.exists(REF_LIB):
+        f = C.CDLL(REF_LIB).gemm_int8
+        f.restype = None
+        f.argtypes = [C.c_void_p] * 3 + [C.c_uint32] * 3 + [C.c_float] * 3 + [C.c_int32] * 2
+        t0 = time.perf_counter()
+        f(a.ctypes.data, b.ctypes.data, out.ctypes.data, rows, n, n, 1.0, 1.0, 1.0, 0, 0)
+        kind = "reference"
+    else:
+        from oracle import Oracle
+
+        orc = Oracle()
+        t0 = time.perf_counter()
+        orc.gemm_int8(a, b, rows, n, n)
+        kind = "port"
     dt = time.perf_counter() - t0
-    return 2.0 * rows * n * n / dt / 1e12, dt
+    return 2.0 * rows * n * n / dt / 1e12, dt, kind
 
 
 def _tensor(lib, arr, requires_grad=False):
@@ -405,14 +424,16 @@ def main():
 
     cpu = None
     if not args.no_cpu and args.only is None:
-        log(f"bench: cpu baseline (oracle, {args.cpu_rows}-row slab)")
+        log(f"bench: cpu baseline ({args.cpu_rows}-row slab)")
         qa = qA.to_array(np.int8, (n, n))
         qb = qB.to_array(np.int8, (n, n))
-        cpu_tops, cpu_s = cpu_baseline_int8(n, args.cpu_rows, qa, qb)
+        cpu_tops, cpu_s, kind = cpu_baseline_int8(n, args.cpu_rows, qa, qb)
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-        cpu = {"value": round(cpu_tops, 6), "unit": "TOP/s", "cores": threads, "kind": "port",
-               "sample": f"oracle gemm_int8 (reference ops_extended.c:83-123 restated, -O3 -fopenmp) on a "
-                         f"{args.cpu_rows}x{n}x{n} row slab of the same quantized inputs, {cpu_s:.1f} s"}
+        what = ("the reference's gemm_int8 (src/ops_extended.c:83-129, built from its sources with -O3 -fopenmp "
+                "into oracle/_ref/libref.so)" if kind == "reference" else
+                "oracle gemm_int8 (reference src/ops_extended.c:83-129 restated, -O3 -fopenmp)")
+        cpu = {"value": round(cpu_tops, 6), "unit": "TOP/s", "cores": threads, "kind": kind,
+               "sample": f"{what} on a {args.cpu_rows}x{n}x{n} row slab of the same quantized inputs, {cpu_s:.1f} s"}
 
     # HBM/MALL bytes per launch of the roofline kernel, from the committed
     # FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel of known size).
