@@ -468,7 +468,7 @@ def main():
                      "kernel": traffic_kernel, "ms_per_launch": round(ms_k, 4)},
         "nt_kernel": nt,
         "roofline_fp32": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
-                          "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4), "kernel": "k_sgemm"},
+                          "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4), "kernel": "k_sgemm_dma<false, false>"},
         "skinny_int8": skinny,
         "configs": configs,
         "cpu_baseline": cpu,
