@@ -11,9 +11,10 @@ uploaded and quantized before the timed region (resident in HBM).
 kernel: gemm_int8 is one launch of the i8-MFMA GEMM kernel that reads B
 [K,N] in place, timed alone with HIP events on its stream (`nt_kernel`
 times the same kernel on B already [N,K], linear_int8's layout);
-`cpu_baseline` times the C oracle (a bit-identical restatement of the
-reference's CPU path) on a 64-row slab of the same INT8 GEMM on the host's
-cores.  Prints ONE JSON line.
+`cpu_baseline` times the reference's own CPU gemm_int8 (built from its
+sources into oracle/_ref/libref.so; the C oracle, a bit-identical
+restatement, when that build is absent) on a 512-row slab of the same INT8
+GEMM on the host's cores.  Prints ONE JSON line.
 """
 import argparse
 import ctypes as C
