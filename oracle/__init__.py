@@ -12,7 +12,7 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_PATH = os.path.join(HERE, "liboracle.so")
+ORACLE_PATH = os.environ.get("RPL_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libref.so")
 
 _vp, _u32, _i32, _f32, _b = C.c_void_p, C.c_uint32, C.c_int32, C.c_float, C.c_bool

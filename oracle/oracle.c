@@ -65,11 +65,14 @@ void orc_gemm_int8(const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, uin
     orc_gemm_int8_rows(A, B, C, M, N, K, sa, sb, sc, za, zb, 0, M);
 }
 
-/* rpl_core.c:521-527 */
+/* rpl_core.c:521-527.  The reference's `(int32_t)roundf(..) + zero_point`
+ * overflows for a NaN / out-of-range value (INT32_MIN) with a negative zero
+ * point; its x86 build wraps (a plain `add`), which is restated here as an
+ * unsigned add so that the oracle itself has no undefined behaviour. */
 void orc_quantize_int8(const float* x, uint32_t n, float scale, int32_t zp, int8_t* q) {
 #pragma omp parallel for
     for (uint32_t i = 0; i < n; i++) {
-        int32_t quantized = (int32_t)roundf(x[i] / scale) + zp;
+        int32_t quantized = (int32_t)((uint32_t)(int32_t)roundf(x[i] / scale) + (uint32_t)zp);
         if (quantized < -128) quantized = -128;
         if (quantized > 127) quantized = 127;
         q[i] = (int8_t)quantized;

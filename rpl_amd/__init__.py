@@ -19,7 +19,9 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
-LIB_PATH = os.path.join(HERE, "librpl.so")
+# RPL_LIB selects another build of the same library (the host sanitizer
+# build, rpl_amd/librpl_san.so, in tests/test_host_sanitizers.py).
+LIB_PATH = os.environ.get("RPL_LIB") or os.path.join(HERE, "librpl.so")
 INCLUDE_DIR = os.path.join(REPO, "include")
 
 MAX_DIMS = 8

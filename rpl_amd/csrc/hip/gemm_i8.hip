@@ -505,14 +505,6 @@ __device__ __forceinline__ void epilogue_tile_full(const EpiParams& p, const v16
 #ifndef RPL_I8_DMA_SLOT
 #define RPL_I8_DMA_SLOT 2
 #endif
-// Big-tile kernel: 0 = one wave per SIMD (k_gemm_i8_nt_dma), 1 = 8-wave
-// ping-pong (k_gemm_i8_nt_pp), and the latter's LDS stages.
-#ifndef RPL_I8_BIG_KERNEL
-#define RPL_I8_BIG_KERNEL 0
-#endif
-#ifndef RPL_I8_PP_STAGES
-#define RPL_I8_PP_STAGES 4
-#endif
 
 namespace dma {
 constexpr int BM = 256, BK = 64, S = RPL_I8_STAGES, kThreads = 256;
@@ -1025,150 +1017,6 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_dma_pairs(const int8_t* __re
     else
         epilogue_tile<EPI, 4, FN, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * (BN / 2) + lane % 32, M,
                                      N);
-}
-
-// --------------------------- NT core GEMM, 8-wave ping-pong (2 waves/SIMD)
-
-namespace pp {
-constexpr int BM = 256, BN = 256, BK = 64, kThreads = 512;
-constexpr int S = RPL_I8_PP_STAGES, D = S - 1;  // LDS stages; tiles requested ahead
-constexpr int kTileBytes = BM * BK, kStageBytes = (BM + BN) * BK;
-constexpr int kLoads = 4;  // 1 KB copies per wave per tile (its group's operand)
-static_assert(S >= 3 && S * kStageBytes <= 160 * 1024, "LDS ring must fit 160 KB");
-}  // namespace pp
-
-// 256 x 256 x 64 tiles, 8 waves: wave w runs on SIMD w%4 and belongs to
-// group g = w/4, so every SIMD hosts one wave of each group.  Each wave owns
-// a 128 x 64 block of the tile (4 x 2 MFMA blocks, 128 accumulators), so two
-// waves fit one SIMD.  The two groups alternate, one barrier apart:
-//
-//   phase 2t-1: group 0 reads its fragments of tile t;  group 1 multiplies tile t-1
-//   phase 2t  : group 0 multiplies tile t;            group 1 reads its fragments of tile t
-//
-// so on every SIMD one wave issues 16 back-to-back MFMAs while the other
-// issues its LDS reads and tile copies, and the roles swap at each barrier
-// with the next wave's operands already in registers.  A memory phase for
-// tile t also requests the wave's share of tile t+D (group 0 copies the A
-// tile, group 1 the B tile, each wave 4 x 1 KB) into the LDS stage that tile
-// t-1 left; each wave waits for its own copies of a tile before the barrier
-// that precedes the tile's first reads.  Copies, swizzle and row clamping as
-// in k_gemm_i8_nt_dma.
-template <int EPI>
-__global__ void __launch_bounds__(512, 1) k_gemm_i8_nt_pp(const int8_t* __restrict__ A, uint32_t lda,
-                                                          const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
-                                                          uint32_t N, uint32_t K, EpiParams p) {
-    using namespace pp;
-    __shared__ __attribute__((aligned(1024))) int8_t smem[S * kStageBytes];
-
-    const uint32_t lane = threadIdx.x % 64;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-    const uint32_t grp = wave / 4, q = wave % 4;
-    const uint32_t wm = q % 2, wn = grp * 2 + q / 2;  // 128-row half, 64-column quarter
-    uint32_t im, in;
-    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, im, in);
-    const uint32_t m0 = im * BM, n0 = in * BN;
-    const uint32_t rows_a = M - m0 < (uint32_t)BM ? M - m0 : BM;
-    const uint32_t rows_b = N - n0 < (uint32_t)BN ? N - n0 : BN;
-
-    // This wave's copies: group 0 the A tile, group 1 the B tile; wave q of
-    // the group copies rows 64q .. 64q+63.
-    const uint32_t rows = grp ? rows_b : rows_a, ld = grp ? ldb : lda;
-    const __amdgpu_buffer_rsrc_t rsrc =
-        grp ? uniform_rsrc(B + (uint64_t)n0 * ldb, rows_b * ldb) : uniform_rsrc(A + (uint64_t)m0 * lda, rows_a * lda);
-    uint32_t voff[kLoads];
-#pragma unroll
-    for (int i = 0; i < kLoads; i++) {
-        const uint32_t r = q * 64 + i * 16 + lane / 4;
-        voff[i] = (r < rows ? r : rows - 1) * ld + ((lane % 4) ^ swz(r)) * 16;
-    }
-    const uint32_t dst = grp * kTileBytes + q * 64 * BK;
-    auto issue = [&](uint32_t kt) {
-        int8_t* st = smem + (kt % S) * kStageBytes + dst;
-#pragma unroll
-        for (int i = 0; i < kLoads; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)(st + i * 16 * BK), 16, voff[i], kt * BK, 0, 0);
-    };
-    // Wait until this wave's copies of tile u have landed when `later` of
-    // its tile shares were requested after tile u's.
-    auto wait_later = [&](uint32_t later) {
-        static_for<D>([&](auto C) {
-            constexpr int c = decltype(C)::value;
-            if (later == (uint32_t)c) __builtin_amdgcn_s_waitcnt(waitcnt_imm(c * kLoads, 0));
-        });
-    };
-
-    // Fragments of both 32-k steps of a tile: A blocks i (rows wm*128 +
-    // 32i + lane%32), B blocks j (rows wn*64 + 32j + lane%32), chunk
-    // 2kk + lane/32 at its swizzled slot (which depends on the lane only).
-    const uint32_t fr = lane % 32;
-    uint32_t foff[2];
-#pragma unroll
-    for (int kk = 0; kk < 2; kk++) foff[kk] = fr * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
-    v4i fa[2][4], fb[2][2];
-    auto fread = [&](uint32_t kt) {
-        const int8_t* st = smem + (kt % S) * kStageBytes;
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++) {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                fa[kk][i] = *reinterpret_cast<const v4i*>(st + foff[kk] + (wm * 128 + i * 32) * BK);
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                fb[kk][j] = *reinterpret_cast<const v4i*>(st + kTileBytes + foff[kk] + (wn * 64 + j * 32) * BK);
-        }
-    };
-    v16i acc[4][2];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = (v16i){};
-    auto mma = [&]() {
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
-    };
-
-    const uint32_t nk = K / BK;
-    // Prologue: tiles 0 .. D-1 requested, tile 0 landed and visible.
-    static_for<D>([&](auto T) {
-        constexpr int t = decltype(T)::value;
-        if (t < nk) issue(t);
-    });
-    wait_later(nk - 1 < (uint32_t)(D - 1) ? nk - 1 : D - 1);
-    __builtin_amdgcn_s_barrier();
-    if (grp == 1) __builtin_amdgcn_s_barrier();  // group 1 starts one phase later
-
-    for (uint32_t t = 0; t < nk; t++) {
-        // Memory phase: fragments of tile t, request tile t+D.
-        __builtin_amdgcn_sched_barrier(0);
-        fread(t);
-        if (t + D < nk) issue(t + D);
-        // Tile t+1 is first read right after the next barrier of group 1 /
-        // the one after of group 0; the wave that reaches it from this phase
-        // (group 1) waits for its copies here, group 0 after its MFMAs.
-        const uint32_t last = t + D < nk - 1 ? t + D : nk - 1;  // last tile requested so far
-        const uint32_t later = last > t + 1 ? last - t - 1 : 0;
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));          // own fragment reads complete
-        if (grp == 1) wait_later(later);
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_barrier();
-        // Compute phase: 16 MFMAs on the fragments in registers.
-        __builtin_amdgcn_sched_barrier(0);
-        mma();
-        __builtin_amdgcn_sched_barrier(0);
-        if (grp == 0) wait_later(later);
-        __builtin_amdgcn_s_barrier();
-    }
-    if (grp == 0) __builtin_amdgcn_s_barrier();  // group 0 ends one phase earlier
-
-    if (m0 + BM <= M && n0 + BN <= N && p.ldc <= kFullEpiMaxLdc)
-        epilogue_tile_full<EPI, 4, 2>(p, acc, m0 + wm * 128, n0 + wn * 64, lane);
-    else
-        epilogue_tile<EPI, 4, 2>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * 64 + lane % 32, M, N);
 }
 
 // --------------------------------------------------- skinny (M <= 16) GEMM
@@ -1765,7 +1613,7 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
         al && K % dma::BK == 0 && (uint64_t)M * lda < (1ull << 31) && (uint64_t)N * ldb < (1ull << 31) && use_dma();
     const uint64_t mt = (M + dma::BM - 1) / dma::BM;
     if (al && use_big_tile(M, N, dma_ok)) {
-        const uint32_t n1 = dma_ok && RPL_I8_BIG_KERNEL != 1 ? balanced_split(M, N) : 0;
+        const uint32_t n1 = dma_ok ? balanced_split(M, N) : 0;
         if (n1) {
             // Columns [0, n1) on big tiles, [n1, N) on 256 x 128 tiles.
             const EpiParams p2 = shift_cols(p, n1);
@@ -1782,10 +1630,7 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
         }
         if (dma_ok) {
             const uint64_t tiles = mt * ((N + 255) / 256);
-            if constexpr (RPL_I8_BIG_KERNEL == 1)
-                hipLaunchKernelGGL((k_gemm_i8_nt_pp<EPI>), dim3((uint32_t)tiles), dim3(pp::kThreads), 0, s, A, lda,
-                                   B, ldb, M, N, K, p);
-            else if (use_pairs(K))
+            if (use_pairs(K))
                 hipLaunchKernelGGL((k_gemm_i8_dma_pairs<EPI, false>), dim3((uint32_t)tiles), dim3(dma::kThreads), 0,
                                    s, A, lda, B, ldb, M, N, K, p);
             else
@@ -1813,7 +1658,7 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
 bool kn_ok(const int8_t* A, const int8_t* B, uint32_t M, uint32_t N, uint32_t K) {
     static const char* env = getenv("RPLHIP_I8_KN");
     if (env && env[0] == '0') return false;
-    if (RPL_I8_BIG_KERNEL == 1 || M <= 16 || K == 0 || K % dma::BK || N % 16 || !aligned16(A) || !aligned16(B))
+    if (M <= 16 || K == 0 || K % dma::BK || N % 16 || !aligned16(A) || !aligned16(B))
         return false;
     if ((uint64_t)M * K >= (1ull << 31) || (uint64_t)K * N >= (1ull << 31)) return false;
     const uint64_t tiles = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);

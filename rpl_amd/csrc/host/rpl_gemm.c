@@ -8,9 +8,15 @@
 
 #include "rpl_host.h"
 
-/* src/rpl_core.c:199-217.  Shapes come from shape[0..1] as in the
- * reference; the operands' inner dimensions must agree (the reference does
- * not check and reads out of bounds when they do not). */
+/* src/rpl_core.c:199-217.  M and K come from A's shape[0..1] and N from
+ * B's, whatever the tensors' ranks, and B's own inner dimension is not
+ * consulted -- exactly as in the reference: it reads A as a dense [M,K]
+ * (or [K,M]) matrix, B as [K,N] (or [N,K]) and C as [M,N], each from its
+ * first elements.  multi_head_attention_forward (src/rpl_attention.c:175-177,
+ * 232) relies on this with 3-D [batch, seq, d_model] tensors (M = batch,
+ * K = seq).  Where the reference stays inside its buffers (M*K, N*K and M*N
+ * within the tensors' sizes) the result is the same; where it would read or
+ * write past them, the call is refused. */
 void tensor_gemm(Tensor* C, const Tensor* A, const Tensor* B, float alpha, float beta, bool trans_a,
                  bool trans_b) {
     if (!C || !A || !B) {
@@ -20,9 +26,10 @@ void tensor_gemm(Tensor* C, const Tensor* A, const Tensor* B, float alpha, float
     uint32_t M = trans_a ? A->shape[1] : A->shape[0];
     uint32_t K = trans_a ? A->shape[0] : A->shape[1];
     uint32_t N = trans_b ? B->shape[0] : B->shape[1];
-    uint32_t Kb = trans_b ? B->shape[1] : B->shape[0];
-    if (A->dims < 2 || B->dims < 2 || Kb != K || (uint64_t)C->size < (uint64_t)M * N) {
-        rpl__bad("tensor_gemm", "shape mismatch: op(A) %ux%u, op(B) %ux%u, C size %u", M, K, Kb, N, C->size);
+    if (A->dims < 2 || B->dims < 2 || (uint64_t)M * K > A->size || (uint64_t)N * K > B->size ||
+        (uint64_t)M * N > C->size) {
+        rpl__bad("tensor_gemm", "out of bounds: op(A) %ux%u of %u, op(B) %ux%u of %u, C %ux%u of %u elements", M, K,
+                 A->size, K, N, B->size, M, N, C->size);
         return;
     }
     if (!rpl_gpu_init()) return;

@@ -103,6 +103,12 @@ void rpl__pool_release_all(void) {
 
 /* ------------------------------------------------ device-buffer registry */
 
+/* Handles index entries held in fixed chunks of kRegChunk that are allocated
+ * once and never move or shrink, so a handle always names the same slot.
+ * Every field is read and written under g_reg_mu, and readers get copies:
+ * no pointer into the table escapes the lock, so a concurrent
+ * tensor_to_gpu (which may add a chunk) or tensor_free cannot leave another
+ * thread with a dangling entry. */
 typedef struct {
     float* data;
     float* grad;
@@ -110,68 +116,101 @@ typedef struct {
     int used;
 } RegEntry;
 
-static pthread_mutex_t g_reg_mu = PTHREAD_MUTEX_INITIALIZER;
-static RegEntry* g_reg;
-static uint32_t g_reg_len, g_reg_cap;
+enum { kRegChunkBits = 10, kRegChunk = 1 << kRegChunkBits, kRegMaxChunks = 4096 };
 
-static RegEntry* reg_get(uint32_t h) {
-    RegEntry* e = NULL;
+static pthread_mutex_t g_reg_mu = PTHREAD_MUTEX_INITIALIZER;
+static RegEntry* g_reg_chunks[kRegMaxChunks];
+static uint32_t g_reg_len; /* slots handed out so far (handles 1..g_reg_len) */
+
+/* Slot of handle h (caller holds g_reg_mu), or NULL for an invalid handle. */
+static RegEntry* reg_slot(uint32_t h) {
+    if (h < 1 || h > g_reg_len) return NULL;
+    RegEntry* e = &g_reg_chunks[(h - 1) >> kRegChunkBits][(h - 1) & (kRegChunk - 1)];
+    return e->used ? e : NULL;
+}
+
+/* Copy of handle h's entry; returns 0 (and a zeroed *out) if it is not live. */
+static int reg_read(uint32_t h, RegEntry* out) {
     pthread_mutex_lock(&g_reg_mu);
-    if (h >= 1 && h <= g_reg_len && g_reg[h - 1].used) e = &g_reg[h - 1];
+    const RegEntry* e = reg_slot(h);
+    if (e) *out = *e;
     pthread_mutex_unlock(&g_reg_mu);
-    return e;
+    if (!e) memset(out, 0, sizeof(*out));
+    return e != NULL;
 }
 
 static uint32_t reg_new(float* data, float* grad, size_t bytes) {
     pthread_mutex_lock(&g_reg_mu);
     uint32_t h = 0;
     for (uint32_t i = 0; i < g_reg_len; i++)
-        if (!g_reg[i].used) {
+        if (!g_reg_chunks[i >> kRegChunkBits][i & (kRegChunk - 1)].used) {
             h = i + 1;
             break;
         }
     if (!h) {
-        if (g_reg_len == g_reg_cap) {
-            uint32_t nc = g_reg_cap ? 2 * g_reg_cap : 256;
-            RegEntry* nr = (RegEntry*)realloc(g_reg, nc * sizeof(RegEntry));
-            if (!nr) {
+        const uint32_t c = g_reg_len >> kRegChunkBits;
+        if (c == kRegMaxChunks) {
+            pthread_mutex_unlock(&g_reg_mu);
+            return 0;
+        }
+        if (!g_reg_chunks[c]) {
+            g_reg_chunks[c] = (RegEntry*)calloc(kRegChunk, sizeof(RegEntry));
+            if (!g_reg_chunks[c]) {
                 pthread_mutex_unlock(&g_reg_mu);
                 return 0;
             }
-            g_reg = nr;
-            g_reg_cap = nc;
         }
         h = ++g_reg_len;
     }
-    g_reg[h - 1].data = data;
-    g_reg[h - 1].grad = grad;
-    g_reg[h - 1].bytes = bytes;
-    g_reg[h - 1].used = 1;
+    RegEntry* e = &g_reg_chunks[(h - 1) >> kRegChunkBits][(h - 1) & (kRegChunk - 1)];
+    e->data = data;
+    e->grad = grad;
+    e->bytes = bytes;
+    e->used = 1;
     pthread_mutex_unlock(&g_reg_mu);
     return h;
 }
 
+/* Retire handle h and return its buffers to the pool.  The entry is taken
+ * out of the table under the lock, so exactly one caller frees them. */
 static void reg_release(uint32_t h) {
-    RegEntry* e = reg_get(h);
-    if (!e) return;
-    rpl__pool_free(e->data, e->bytes);
-    if (e->grad) rpl__pool_free(e->grad, e->bytes);
+    RegEntry copy = {0};
     pthread_mutex_lock(&g_reg_mu);
-    e->used = 0;
-    e->data = e->grad = NULL;
+    RegEntry* e = reg_slot(h);
+    if (e) {
+        copy = *e;
+        e->used = 0;
+        e->data = e->grad = NULL;
+    }
     pthread_mutex_unlock(&g_reg_mu);
+    if (!copy.used) return;
+    rpl__pool_free(copy.data, copy.bytes);
+    if (copy.grad) rpl__pool_free(copy.grad, copy.bytes);
 }
 
-int rpl__is_gpu(const Tensor* t) { return t && t->device == DEVICE_GPU && reg_get(t->gpu_buffer) != NULL; }
+static int reg_read_tensor(const Tensor* t, RegEntry* out) {
+    if (!t || t->device != DEVICE_GPU) {
+        memset(out, 0, sizeof(*out));
+        return 0;
+    }
+    return reg_read(t->gpu_buffer, out);
+}
+
+int rpl__is_gpu(const Tensor* t) {
+    RegEntry e;
+    return reg_read_tensor(t, &e);
+}
 
 float* rpl__dev_data(const Tensor* t) {
-    RegEntry* e = (t && t->device == DEVICE_GPU) ? reg_get(t->gpu_buffer) : NULL;
-    return e ? e->data : NULL;
+    RegEntry e;
+    reg_read_tensor(t, &e);
+    return e.data;
 }
 
 float* rpl__dev_grad(const Tensor* t) {
-    RegEntry* e = (t && t->device == DEVICE_GPU) ? reg_get(t->gpu_buffer) : NULL;
-    return e ? e->grad : NULL;
+    RegEntry e;
+    reg_read_tensor(t, &e);
+    return e.grad;
 }
 
 int rpl__attach(Tensor* t, int upload) {
@@ -207,19 +246,30 @@ int rpl__attach(Tensor* t, int upload) {
 }
 
 int rpl__attach_grad(Tensor* t) {
-    RegEntry* e = (t && t->device == DEVICE_GPU) ? reg_get(t->gpu_buffer) : NULL;
-    if (!e) return 0;
-    if (e->grad) return 1;
-    float* g = (float*)rpl__pool_alloc(e->bytes);
+    RegEntry e;
+    if (!reg_read_tensor(t, &e)) return 0;
+    if (e.grad) return 1;
+    float* g = (float*)rpl__pool_alloc(e.bytes);
     if (!g) return 0;
-    if (!rpl__ok(rplhip_memset(g, 0, e->bytes, NULL), "device gradient")) {
-        rpl__pool_free(g, e->bytes);
+    if (!rpl__ok(rplhip_memset(g, 0, e.bytes, NULL), "device gradient")) {
+        rpl__pool_free(g, e.bytes);
         return 0;
     }
+    /* Install by handle under the lock; if another thread installed one (or
+     * released the tensor) meanwhile, keep the table as it is. */
+    int installed = 0, live = 0;
     pthread_mutex_lock(&g_reg_mu);
-    e->grad = g;
+    RegEntry* s = reg_slot(t->gpu_buffer);
+    if (s) {
+        live = 1;
+        if (!s->grad) {
+            s->grad = g;
+            installed = 1;
+        }
+    }
     pthread_mutex_unlock(&g_reg_mu);
-    return 1;
+    if (!installed) rpl__pool_free(g, e.bytes);
+    return live;
 }
 
 /* ---------------------------------------------------------------- staging */

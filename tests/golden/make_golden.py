@@ -141,6 +141,23 @@ def main():
     for t in (tA, tB, tC):
         L.tensor_free(t)
 
+    # ---- tensor_gemm on multi_head_attention_forward's 3-D projections
+    # (rpl_attention.c:175-177,232): C [b,s,d] zero-filled, A [b,s,d],
+    # W [d,d], trans_b, alpha 1, beta 0.  tensor_gemm reads shape[0..1] only,
+    # so M = b, K = s, N = d: it multiplies the first b*s values of A, taken
+    # as a [b,s] matrix, by the first d*s values of W, taken as [d,s], into
+    # the first b*d values of C; every read stays in bounds when s <= d.
+    for name, (bb, ss, dd) in (("mha_s5_d8", (2, 5, 8)), ("mha_s8_d8", (3, 8, 8)), ("mha_s3_d16", (4, 3, 16))):
+        X3 = rpl_amd.fill_uniform(bb * ss * dd, seed(90, 3)).reshape(bb, ss, dd)
+        W = rpl_amd.fill_uniform(dd * dd, seed(90, 4)).reshape(dd, dd)
+        tX, tW = ref.tensor(X3), ref.tensor(W)
+        tC = ref.tensor(np.zeros((bb, ss, dd), np.float32))
+        L.tensor_gemm(tC, tX, tW, 1.0, 0.0, False, True)
+        g[f"sgemm3d_{name}_A"], g[f"sgemm3d_{name}_W"] = X3, W
+        g[f"sgemm3d_{name}_C"] = ref.data(tC).reshape(bb, ss, dd)
+        for t in (tX, tW, tC):
+            L.tensor_free(t)
+
     # ---- parallel_gemm_optimized at N == 4, where the reference kernel is
     # correct (C += A*B); pins the entry point's intended semantics.
     M, N, K = 8, 4, 16

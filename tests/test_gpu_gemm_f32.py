@@ -235,6 +235,45 @@ def test_tensor_gemm_api(gpu, orc, golden, resident):
             lib.tensor_free(t)
 
 
+@pytest.mark.parametrize("resident", [False, True])
+@pytest.mark.parametrize("name", ["mha_s5_d8", "mha_s8_d8", "mha_s3_d16"])
+def test_tensor_gemm_3d_projection(gpu, golden, name, resident):
+    """multi_head_attention_forward's projections (src/rpl_attention.c:175-177,
+    232): tensor_gemm on [b,s,d] tensors with W [d,d] and trans_b takes
+    M = b, K = s, N = d from shape[0..1].  Reference golden, bit-exact (K <= 256:
+    the reference's operation order)."""
+    lib = gpu
+    A, W, want = golden[f"sgemm3d_{name}_A"], golden[f"sgemm3d_{name}_W"], golden[f"sgemm3d_{name}_C"]
+    tA, tW, tC = tensor_from(lib, A), tensor_from(lib, W), tensor_from(lib, np.zeros(A.shape, np.float32))
+    if resident:
+        for t in (tA, tW, tC):
+            lib.tensor_to_gpu(t)
+    say("tensor_gemm 3-D", name, "resident" if resident else "host")
+    lib.tensor_gemm(tC, tA, tW, 1.0, 0.0, False, True)
+    if resident:
+        lib.tensor_from_gpu(tC)
+    assert not lib.rpl_last_error()
+    assert bits_equal(tensor_data(tC, A.shape), want)
+    for t in (tA, tW, tC):
+        lib.tensor_free(t)
+
+
+def test_tensor_gemm_out_of_bounds_refused(gpu):
+    """Where the reference would read past a buffer (seq > d_model: N*K
+    exceeds W's size) the call is refused and C is left untouched."""
+    lib = gpu
+    A = np.ones((2, 9, 8), np.float32)
+    W = np.ones((8, 8), np.float32)
+    C0 = np.full((2, 9, 8), 3.0, np.float32)
+    tA, tW, tC = tensor_from(lib, A), tensor_from(lib, W), tensor_from(lib, C0)
+    say("tensor_gemm out of bounds")
+    lib.tensor_gemm(tC, tA, tW, 1.0, 0.0, False, True)
+    assert b"out of bounds" in lib.rpl_last_error()
+    assert bits_equal(tensor_data(tC, C0.shape), C0)
+    for t in (tA, tW, tC):
+        lib.tensor_free(t)
+
+
 def test_tensor_matmul_and_matmul_gpu(gpu, orc):
     lib = gpu
     rng = np.random.default_rng(8)

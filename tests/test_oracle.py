@@ -39,6 +39,25 @@ def test_sgemm_nan_in_c_propagates(orc, golden):
     assert np.isnan(out[1, 2]) and np.isfinite(out[0, 0])
 
 
+MHA_CASES = ["mha_s5_d8", "mha_s8_d8", "mha_s3_d16"]
+
+
+@pytest.mark.parametrize("name", MHA_CASES)
+def test_sgemm_3d_projection_golden(orc, golden, name):
+    # tensor_gemm on multi_head_attention_forward's [b,s,d] tensors
+    # (rpl_attention.c:175-177): M = b, K = s, N = d from shape[0..1], the
+    # first b*s values of A against the first d*s of W, into the first b*d
+    # values of C; the rest of C keeps its zeros.
+    A, W, want = golden[f"sgemm3d_{name}_A"], golden[f"sgemm3d_{name}_W"], golden[f"sgemm3d_{name}_C"]
+    b, s, d = A.shape
+    out = orc.sgemm(A.reshape(-1)[:b * s], W.reshape(-1)[:d * s], np.zeros((b, d), np.float32), b, d, s, tb=True)
+    assert bits_equal(out.reshape(-1), want.reshape(-1)[:b * d])
+    assert not want.reshape(-1)[b * d:].any()
+    # The same product in float64 (closed form of the dense reading).
+    ref = A.reshape(-1)[:b * s].astype(np.float64).reshape(b, s) @ W.reshape(-1)[:d * s].astype(np.float64).reshape(d, s).T
+    assert np.max(np.abs(out - ref)) <= 1e-6 * s
+
+
 def test_gemm_optimized_intended_semantics(orc, golden):
     # parallel_gemm_optimized is C += A*B: tensor_gemm with alpha = beta = 1.
     A, B, C0 = golden["gemmopt_A"], golden["gemmopt_B"], golden["gemmopt_C0"]
