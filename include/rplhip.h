@@ -98,6 +98,20 @@ int rplhip_gemm_int8(const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, u
                      uint32_t K, float sa, float sb, float sc, int32_t za, int32_t zb,
                      rplhip_stream_t stream);
 
+/* No counterpart in the reference: rplhip_gemm_int8 (same arguments, same
+ * results bit for bit) for callers that cannot allocate device memory --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  It calls no hipMalloc, hipFree or allocating library routine:
+ * its scratch (B transposed, K*N bytes, when B cannot be read in place, plus
+ * 4*(M+N) bytes of zero-point sums) is a static 16 MiB device array per GPU,
+ * held until the process ends.  Calls needing more than 16 MiB of scratch
+ * fail with RPLHIP_ERR_UNSUPPORTED.  All calls on one GPU share the array:
+ * calls on one stream are ordered and safe, calls that overlap on one GPU
+ * (different streams) race. */
+int rplhip_gemm_int8_noalloc(const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, uint32_t N,
+                             uint32_t K, float sa, float sb, float sc, int32_t za, int32_t zb,
+                             rplhip_stream_t stream);
+
 /* linear_int8 (src/rpl_quantization.c:314-353): X [M,K] int8, W [N,K] int8
  * (Linear layout), out[m,n] = sum_k X[m,k] W[n,k] (+ bias[n] if bias != NULL),
  * int32.  Zero points are ignored, as in the reference.  M <= 16 runs the

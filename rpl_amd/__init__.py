@@ -189,6 +189,7 @@ PROTOTYPES = {
     "rplhip_sgemm_batched": (_int, [_int, _int, _u32, _u32, _u32, _f32, _vp, _u32, _u64, _vp, _u32, _u64, _f32, _vp,
                                     _u32, _u64, _u32, _int, _vp]),
     "rplhip_gemm_int8": (_int, [_vp, _vp, _vp, _u32, _u32, _u32, _f32, _f32, _f32, _i32, _i32, _vp]),
+    "rplhip_gemm_int8_noalloc": (_int, [_vp, _vp, _vp, _u32, _u32, _u32, _f32, _f32, _f32, _i32, _i32, _vp]),
     "rplhip_linear_int8": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "rplhip_linear_int8_dequant": (_int, [_vp, _vp, _int, _vp, _vp, _int, _vp, _u32, _u32, _u32, _vp]),
     "rplhip_gemm_int8_dequant": (_int, [_vp, _vp, _int, _vp, _vp, _int, _vp, _u32, _u32, _u32, _vp]),

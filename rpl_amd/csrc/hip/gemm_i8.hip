@@ -32,6 +32,7 @@
 //                  host (no NaN, no overflow): no divide and no range test
 //   kDequant     : y = ((float)acc * sx[m|0]) * sw[n|0]       (fused fp32 output)
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 
 #include <type_traits>
@@ -1712,6 +1713,93 @@ int transpose_b(const int8_t* B, uint32_t K, uint32_t N, int8_t* Bt, hipStream_t
     return rplhip::check_launch("int8 transpose");
 }
 
+// gemm_int8's B is read in place when the kernel can (the column sums of a
+// zero point of B come from the transposed copy).
+bool gemm_int8_reads_b_in_place(const int8_t* A, const int8_t* B, uint32_t M, uint32_t N, uint32_t K, int32_t za) {
+    return za == 0 && kn_ok(A, B, M, N, K);
+}
+
+// Device scratch bytes of one gemm_int8 call: the transposed copy of B
+// (unless B is read in place), then A's row sums (zb != 0) and B's column
+// sums (za != 0).
+size_t gemm_int8_scratch_bytes(bool kn, uint32_t M, uint32_t N, uint32_t K, int32_t za, int32_t zb) {
+    const size_t bt = kn ? 0 : ((size_t)K * N + 15) / 16 * 16;
+    return bt + sizeof(int32_t) * ((za ? (size_t)N : 0) + (zb ? (size_t)M : 0)) + 16;
+}
+
+// gemm_int8 on scratch `ws` of at least gemm_int8_scratch_bytes(kn, ...).
+int gemm_int8_run(const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, uint32_t N, uint32_t K, float sa,
+                  float sb, float sc, int32_t za, int32_t zb, bool kn, void* ws, hipStream_t s) {
+    const size_t bt_bytes = kn ? 0 : ((size_t)K * N + 15) / 16 * 16;
+    int8_t* Bt = (int8_t*)ws;
+    int32_t* sum_ptr = (int32_t*)((char*)ws + bt_bytes);
+    EpiParams p = {};
+    p.out_i32 = C;
+    p.ldc = N;
+    p.sa = sa;
+    p.sb = sb;
+    p.sc = sc;
+    p.za = za;
+    p.zb = zb;
+    p.kzz = (int32_t)((uint32_t)K * (uint32_t)za * (uint32_t)zb);
+    int st = RPLHIP_OK;
+    if (K && !kn) st = transpose_b(B, K, N, Bt, s);
+    if (!st && zb && K) {
+        p.rowsum_a = sum_ptr;
+        sum_ptr += M;
+        hipLaunchKernelGGL(k_rowsum_i8, dim3(M), dim3(256), 0, s, A, M, K, (int32_t*)p.rowsum_a);
+        st = rplhip::check_launch("int8 row sums");
+    }
+    if (!st && za && K) {
+        p.rowsum_b = sum_ptr;
+        hipLaunchKernelGGL(k_rowsum_i8, dim3(N), dim3(256), 0, s, Bt, N, K, (int32_t*)p.rowsum_b);
+        st = rplhip::check_launch("int8 column sums");
+    }
+    if (st) return st;
+    if (za == 0 && zb == 0 && sc == 1.0f && requant_in_range(K, sa, sb))
+        return kn ? launch_kn<kRequantUnit>(A, B, M, N, K, p, s) : run_nt<kRequantUnit>(A, K, Bt, K, M, N, K, p, s);
+    if (za == 0 && zb == 0 && exact_reciprocal(sc, &p.inv_sc))
+        return kn ? launch_kn<kRequantPow2>(A, B, M, N, K, p, s) : run_nt<kRequantPow2>(A, K, Bt, K, M, N, K, p, s);
+    return kn ? launch_kn<kRequant>(A, B, M, N, K, p, s) : run_nt<kRequant>(A, K, Bt, K, M, N, K, p, s);
+}
+
+// Static scratch of rplhip_gemm_int8_noalloc.  Device code never names the
+// array: kernels get its address as an argument, like a workspace.  On the
+// host `scratch` is only a stand-in symbol (a kernel given it would fault);
+// the device address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+constexpr int kMaxDevices = 64;
+pthread_mutex_t g_scratch_mu = PTHREAD_MUTEX_INITIALIZER;
+void* g_scratch_ptr[kMaxDevices];
+
+}  // namespace
+
+static __device__ __align__(256) int8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+// Device address of `scratch` on the current device (looked up on the
+// device's first call, then cached).
+int noalloc_scratch(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return rplhip::fail(RPLHIP_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "device %d out of range", dev);
+    pthread_mutex_lock(&g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            pthread_mutex_unlock(&g_scratch_mu);
+            return rplhip::fail(RPLHIP_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    pthread_mutex_unlock(&g_scratch_mu);
+    return RPLHIP_OK;
+}
+
 }  // namespace
 
 using namespace rplhip;
@@ -1753,47 +1841,38 @@ int rplhip_gemm_int8(const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, u
     if (!C || (K && (!A || !B))) return fail(RPLHIP_ERR_INVALID, "rplhip_gemm_int8: NULL pointer");
     RPLHIP_REQUIRE_DEVICE();
     hipStream_t s = as_stream(stream);
-    // B is read in place when the kernel can (the column sums of a zero
-    // point of B come from the transposed copy).
-    const bool kn = za == 0 && kn_ok(A, B, M, N, K);
-    size_t bt_bytes = kn ? 0 : ((size_t)K * N + 15) / 16 * 16;
-    size_t sums = (za ? (size_t)N : 0) + (zb ? (size_t)M : 0);
+    const bool kn = gemm_int8_reads_b_in_place(A, B, M, N, K, za);
     void* ws = nullptr;
-    int st = ws_alloc(&ws, bt_bytes + sizeof(int32_t) * sums + 16, s);
+    int st = ws_alloc(&ws, gemm_int8_scratch_bytes(kn, M, N, K, za, zb), s);
     if (st) return st;
-    int8_t* Bt = (int8_t*)ws;
-    int32_t* sum_ptr = (int32_t*)((char*)ws + bt_bytes);
-    EpiParams p = {};
-    p.out_i32 = C;
-    p.ldc = N;
-    p.sa = sa;
-    p.sb = sb;
-    p.sc = sc;
-    p.za = za;
-    p.zb = zb;
-    p.kzz = (int32_t)((uint32_t)K * (uint32_t)za * (uint32_t)zb);
-    if (K && !kn) st = transpose_b(B, K, N, Bt, s);
-    if (!st && zb && K) {
-        p.rowsum_a = sum_ptr;
-        sum_ptr += M;
-        hipLaunchKernelGGL(k_rowsum_i8, dim3(M), dim3(256), 0, s, A, M, K, (int32_t*)p.rowsum_a);
-        st = check_launch("int8 row sums");
-    }
-    if (!st && za && K) {
-        p.rowsum_b = sum_ptr;
-        hipLaunchKernelGGL(k_rowsum_i8, dim3(N), dim3(256), 0, s, Bt, N, K, (int32_t*)p.rowsum_b);
-        st = check_launch("int8 column sums");
-    }
-    if (!st) {
-        if (za == 0 && zb == 0 && sc == 1.0f && requant_in_range(K, sa, sb))
-            st = kn ? launch_kn<kRequantUnit>(A, B, M, N, K, p, s) : run_nt<kRequantUnit>(A, K, Bt, K, M, N, K, p, s);
-        else if (za == 0 && zb == 0 && exact_reciprocal(sc, &p.inv_sc))
-            st = kn ? launch_kn<kRequantPow2>(A, B, M, N, K, p, s) : run_nt<kRequantPow2>(A, K, Bt, K, M, N, K, p, s);
-        else
-            st = kn ? launch_kn<kRequant>(A, B, M, N, K, p, s) : run_nt<kRequant>(A, K, Bt, K, M, N, K, p, s);
-    }
+    st = gemm_int8_run(A, B, C, M, N, K, sa, sb, sc, za, zb, kn, ws, s);
     ws_free(ws, s);
     return st;
+}
+
+// gemm_int8 with its scratch (the transposed copy of B and the zero-point
+// sums) in the library's static device array instead of a workspace
+// allocation: no hipMalloc, hipFree or allocating library call.  Every call
+// on a device shares that device's array, so calls that overlap in time on
+// one device (different streams, no ordering between them) race; calls on
+// one stream are ordered and safe.  Every byte of scratch a call reads is
+// written by the same call first, so nothing needs clearing.
+int rplhip_gemm_int8_noalloc(const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, uint32_t N, uint32_t K,
+                             float sa, float sb, float sc, int32_t za, int32_t zb, rplhip_stream_t stream) {
+    if (M == 0 || N == 0) return RPLHIP_OK;
+    if (!C || (K && (!A || !B))) return fail(RPLHIP_ERR_INVALID, "rplhip_gemm_int8_noalloc: NULL pointer");
+    RPLHIP_REQUIRE_DEVICE();
+    const bool kn = gemm_int8_reads_b_in_place(A, B, M, N, K, za);
+    const size_t need = gemm_int8_scratch_bytes(kn, M, N, K, za, zb);
+    if (need > kNoAllocScratchBytes)
+        return fail(RPLHIP_ERR_UNSUPPORTED,
+                    "rplhip_gemm_int8_noalloc: %u x %u x %u (za %d, zb %d) needs %zu bytes of scratch, more than "
+                    "the %zu-byte static scratch",
+                    M, N, K, za, zb, need, kNoAllocScratchBytes);
+    void* ws = nullptr;
+    int st = noalloc_scratch(&ws);
+    if (st) return st;
+    return gemm_int8_run(A, B, C, M, N, K, sa, sb, sc, za, zb, kn, ws, as_stream(stream));
 }
 
 int rplhip_gemm_int8_dequant(const int8_t* A, const float* a_scale, int a_per_row, const int8_t* B,
