@@ -8,9 +8,12 @@ same way and reported beside it.  Inputs are generated from fixed seeds,
 uploaded and quantized before the timed region (resident in HBM).
 
 `value` is the INT8 throughput in TOP/s.  `roofline` covers the dominant
-kernel: gemm_int8 is one launch of the i8-MFMA GEMM kernel that reads B
-[K,N] in place, timed alone with HIP events on its stream (`nt_kernel`
-times the same kernel on B already [N,K], linear_int8's layout);
+kernel: at 8192^3 gemm_int8 is exactly one launch of the i8-MFMA GEMM
+kernel that reads B [K,N] in place, so the headline leg's HIP-event time on
+its stream is that kernel's average launch duration (`nt_kernel` times the
+same kernel on B already [N,K], linear_int8's layout); `power` samples the
+socket power and shader clock (sysfs hwmon) while the INT8 and FP32 GEMMs
+run back to back, untimed;
 `cpu_baseline` times the reference's own CPU gemm_int8 (built from its
 sources into oracle/_ref/libref.so; the C oracle, a bit-identical
 restatement, when that build is absent) on a 512-row slab of the same INT8
@@ -44,6 +47,97 @@ def seed(cfg, stream):
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def _hwmon_dirs():
+    import glob
+    return sorted(glob.glob("/sys/class/drm/card*/device/hwmon/hwmon*"))
+
+
+def _read(path):
+    try:
+        with open(path) as f:
+            return f.read()
+    except OSError:
+        return None
+
+
+def _sample_power_clock():
+    """(socket W, shader clock MHz) of the first GPU that reports both, from
+    hwmon power1_input (uW) and the active level of pp_dpm_sclk."""
+    for d in _hwmon_dirs():
+        pw = _read(os.path.join(d, "power1_input")) or _read(os.path.join(d, "power1_average"))
+        sclk = _read(os.path.join(os.path.dirname(os.path.dirname(d)), "pp_dpm_sclk"))
+        if pw is None or sclk is None:
+            continue
+        mhz = None
+        for line in sclk.splitlines():
+            if line.strip().endswith("*"):
+                mhz = float(line.split(":")[1].strip().rstrip("*").strip().lower().replace("mhz", ""))
+        return int(pw) / 1e6, mhz
+    return None, None
+
+
+def power_while(lib, stream, fn, seconds):
+    """Run fn back to back on `stream` for `seconds` (untimed) while a thread
+    samples socket power and shader clock every 50 ms; medians over the
+    second half.  The GPU never idles: each batch is queued before the host
+    waits for the previous one, and the last batch is still running when
+    this returns, so a timed leg queued next starts with no idle gap (an idle
+    gap of a few ms on a power-capped MI355X is followed by a clock dip that
+    lasts ~20 launches of the 8192^3 INT8 GEMM)."""
+    import threading
+
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            samples.append(_sample_power_clock())
+            stop.wait(0.05)
+
+    ev = [C.c_void_p(), C.c_void_p()]
+    for e in ev:
+        check(lib.rplhip_event_create(C.byref(e)))
+    _KEEP.extend(ev)  # destroyed never: the last one may still be pending on return
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn()
+        check(lib.rplhip_event_record(ev[i % 2], stream))
+        if i:
+            check(lib.rplhip_event_synchronize(ev[(i - 1) % 2]))
+        i += 1
+    for _ in range(16):  # keep the GPU busy through the bookkeeping below and the caller's next launches
+        fn()
+    stop.set()  # the sampler ends by itself; no join while the GPU must stay busy
+    got = list(samples)
+    tail = [s for s in got[len(got) // 2:] if s[0] is not None]
+    if not tail:
+        return None
+    med = lambda v: float(np.median([x for x in v if x is not None])) if any(x is not None for x in v) else None  # noqa
+    return {"socket_W": round(med([s[0] for s in tail]), 1), "sclk_MHz": med([s[1] for s in tail]),
+            "samples": len(tail), "seconds": seconds,
+            "source": "hwmon power1_input and the active pp_dpm_sclk level, median of the second half"}
+
+
+_KEEP = []
+
+
+def host_cpu():
+    """Host CPU model and the cores this process may run on."""
+    model = None
+    for line in (_read("/proc/cpuinfo") or "").splitlines():
+        if line.startswith("model name"):
+            model = line.split(":", 1)[1].strip()
+            break
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
+    return model, affinity
 
 
 class Timer:
@@ -282,10 +376,11 @@ def main():
     ap.add_argument("--n", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=512)
-    ap.add_argument("--settle-ms", type=float, default=300.0,
-                    help="untimed gemm_int8 work before the first timed leg: the first ~100 ms of load on an idle "
-                         "MI355X run at boost clock and then through a power-management dip")
-    ap.add_argument("--only", choices=["int8", "int8-kernel", "int8-nt", "fp32", "skinny", "configs"],
+    ap.add_argument("--settle-ms", type=float, default=1000.0,
+                    help="untimed gemm_int8 work before the first timed leg (power and clock are sampled during "
+                         "it): the first ~100 ms of load on an idle MI355X run at boost clock and then through a "
+                         "power-management dip")
+    ap.add_argument("--only", choices=["int8", "int8-nt", "fp32", "skinny", "configs"],
                     help="run one leg only (for profiling); the JSON line then has nulls for the rest")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -323,24 +418,17 @@ def main():
 
     want = lambda leg: args.only in (None, leg)  # noqa: E731
     # Let the power state settle (measured: the first ~25 back-to-back calls
-    # after idle run 496 -> 644 -> 515 us) so every leg sees steady state.
-    t_end = time.perf_counter() + args.settle_ms * 1e-3
-    while time.perf_counter() < t_end:
-        for _ in range(20):
-            int8_step()
-        check(lib.rplhip_synchronize())
-    ms_i8 = wall_i8 = tops = ms_k = kern_tops = ms_f32 = wall_f32 = tflops = float("nan")
+    # after idle run 496 -> 644 -> 515 us) so every leg sees steady state;
+    # the socket power and shader clock are sampled meanwhile.
+    power = {"int8": power_while(lib, stream, int8_step, args.settle_ms * 1e-3)}
+    ms_i8 = wall_i8 = tops = ms_f32 = wall_f32 = tflops = float("nan")
     if want("int8"):
+        # At 8192^3 gemm_int8 is exactly one kernel launch
+        # (k_gemm_i8_dma_pairs<kRequantUnit, BKN>, B [K,N] read in place), so
+        # these HIP events on its stream time that kernel alone.
         log("bench: int8 gemm_int8 8192^3")
         ms_i8, wall_i8 = timer.time(int8_step, args.steps, args.warmup)
         tops = ops / (ms_i8 * 1e-3) / 1e12
-
-    # Dominant kernel alone: gemm_int8 launches exactly one kernel
-    # (k_gemm_i8_dma_pairs with B [K,N] read in place), timed on its stream.
-    if want("int8-kernel") or args.only is None:
-        log("bench: int8 GEMM kernel alone")
-        ms_k, _ = timer.time(int8_step, args.steps, args.warmup)
-        kern_tops = ops / (ms_k * 1e-3) / 1e12
     # The same kernel on B already [N,K] (linear_int8's layout, raw int32).
     nt = None
     if want("int8-nt") or args.only is None:
@@ -361,6 +449,9 @@ def main():
         log("bench: fp32 sgemm 8192^3")
         ms_f32, wall_f32 = timer.time(fp32_step, max(args.steps // 2, 3), 2)
         tflops = ops / (ms_f32 * 1e-3) / 1e12
+        if args.only is None:
+            power["fp32"] = power_while(lib, stream, fp32_step, 0.5)
+            check(lib.rplhip_synchronize())
 
     # ---- skinny INT8 (M in {1,4,16}, K=N=8192, per-channel W): HBM-bound.
     # Rotate 6 distinct 64 MiB weight copies (> 256 MB MALL) across calls.
@@ -429,12 +520,15 @@ def main():
         qa = qA.to_array(np.int8, (n, n))
         qb = qB.to_array(np.int8, (n, n))
         cpu_tops, cpu_s, kind = cpu_baseline_int8(n, args.cpu_rows, qa, qb)
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        model, affinity = host_cpu()
+        threads = int(os.environ.get("OMP_NUM_THREADS") or affinity or 1)
         what = ("the reference's gemm_int8 (src/ops_extended.c:83-129, built from its sources with -O3 -fopenmp "
                 "into oracle/_ref/libref.so)" if kind == "reference" else
                 "oracle gemm_int8 (reference src/ops_extended.c:83-129 restated, -O3 -fopenmp)")
         cpu = {"value": round(cpu_tops, 6), "unit": "TOP/s", "cores": threads, "kind": kind,
-               "sample": f"{what} on a {args.cpu_rows}x{n}x{n} row slab of the same quantized inputs, {cpu_s:.1f} s"}
+               "sample": f"{what} on a {args.cpu_rows}x{n}x{n} row slab of the same quantized inputs, {cpu_s:.1f} s",
+               "cpu_model": model, "affinity_cores": affinity,
+               "threads": "OpenMP, OMP_NUM_THREADS (else every core in the affinity mask)"}
 
     # HBM/MALL bytes per launch of the roofline kernel, from the committed
     # FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel of known size).
@@ -464,16 +558,17 @@ def main():
         "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2),
         "fp32": {"value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(ms_f32, 4),
                  "pct_peak": round(100 * tflops / PEAK_FP32_TFLOPS, 2), "dtype": "f32"},
-        "roofline": {"bound": "mfma", "achieved": round(kern_tops, 2), "peak": PEAK_INT8_TOPS,
-                     "unit": "TFLOP/s", "frac": round(kern_tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
-                     "kernel": traffic_kernel, "ms_per_launch": round(ms_k, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS,
+                     "unit": "TOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
+                     "kernel": traffic_kernel, "ms_per_launch": round(ms_i8, 4)},
         "nt_kernel": nt,
         "roofline_fp32": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4), "kernel": "k_sgemm_dma<false, false>"},
         "skinny_int8": skinny,
         "configs": configs,
         "cpu_baseline": cpu,
-        "device": {"arch": arch.value.decode(), "cus": cus.value, "clock_mhz": clk.value // 1000},
+        "device": {"arch": arch.value.decode(), "cus": cus.value, "clock_mhz_max": clk.value // 1000},
+        "power": power,
         "wall_s": {"int8": round(wall_i8, 3), "fp32": round(wall_f32, 3)},
         "settle_ms": args.settle_ms,
     }
