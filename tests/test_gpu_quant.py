@@ -157,12 +157,40 @@ def test_quantize_unaligned_pointers(gpu, orc):
     assert bits_equal(got, orc.quantize_int8(x, 0.05, 0))
 
 
-@pytest.mark.parametrize("rows,cols", [(4096, 4096), (8192, 8192), (33, 1001), (3, 9000), (1, 64)])
+# Rows of up to 8192 floats with cols % 4 == 0 and aligned rows are held in
+# registers (k_quantize_rows<true>: whole and partial 1024-float passes of
+# the block), others are read twice (k_quantize_rows<false>: 33 x 1001,
+# 3 x 9000, odd row starts).
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (8192, 8192), (33, 1001), (3, 9000), (1, 64), (2048, 4096),
+                                       (7, 4112), (5, 16), (9, 1004), (6, 8192), (13, 2060), (3, 4)])
 def test_per_channel_vs_oracle(gpu, orc, rows, cols):
     x = rpl_amd.fill_normal(rows * cols, seed(94, 7)).reshape(rows, cols)
     say("per-channel", rows, cols)
     q, s = dev_per_channel(gpu, x, rows)
     oq, os_ = orc.quantize_per_channel(x, rows)
+    assert bits_equal(q, oq.reshape(-1)) and bits_equal(s, os_)
+
+
+@pytest.mark.parametrize("cols", [48, 4096, 6164])
+def test_per_channel_special_rows(gpu, orc, cols):
+    """Rows that are all zero (scale 0: 0/0 -> -128), hold NaN (never the
+    min or max; NaN / scale -> -128), +-inf (scale inf), signed zeros, exact
+    .5 ties and the largest finite floats."""
+    rng = np.random.default_rng(cols)
+    x = rng.standard_normal((8, cols)).astype(np.float32)
+    x[0] = 0.0
+    x[1, 5] = np.nan
+    x[2, 3] = np.inf
+    x[3, :] = -0.0
+    x[3, 7] = 0.0
+    x[4, :4] = [127.0, 63.5, -63.5, 0.5]
+    x[5, 1] = np.finfo(np.float32).max
+    x[5, 2] = -np.finfo(np.float32).max
+    x[6, :] = np.nan
+    x[7, 9] = -np.inf
+    say("per-channel special rows", cols)
+    q, s = dev_per_channel(gpu, x, 8)
+    oq, os_ = orc.quantize_per_channel(x, 8)
     assert bits_equal(q, oq.reshape(-1)) and bits_equal(s, os_)
 
 
