@@ -17,6 +17,7 @@
 #include <stdlib.h>
 
 #include "mfma_pipe.h"
+#include "rplhip_internal.h"
 
 namespace {
 
@@ -561,10 +562,13 @@ __global__ void __launch_bounds__(256, 1) k_sgemm_dma(uint32_t M, uint32_t N, ui
 }
 
 // C = alpha * sum_s W[s] + beta * C over the split partials W[s] ([M, N],
-// ld N), summed in split order (deterministic).
+// ld N), summed in split order (deterministic).  With a bias, also
+// out2 = C + bias[n] (linear_forward's broadcast add, a separately rounded
+// float add as src/rpl_core.c:112-120 does it).
 __global__ void __launch_bounds__(256) k_splitk_reduce(const float* __restrict__ W, uint32_t splits, uint32_t M,
                                                        uint32_t N, float alpha, float beta, float* __restrict__ C,
-                                                       uint32_t ldc, int read_c) {
+                                                       uint32_t ldc, int read_c, const float* __restrict__ bias,
+                                                       float* __restrict__ out2) {
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (uint64_t)M * N) return;
     const uint32_t m = (uint32_t)(i / N), n = (uint32_t)(i % N);
@@ -582,7 +586,9 @@ __global__ void __launch_bounds__(256) k_splitk_reduce(const float* __restrict__
     }
     for (; s < splits; s++) sum += W[(uint64_t)s * stride + i];
     float* cp = &C[(uint64_t)m * ldc + n];
-    *cp = alpha * sum + (read_c ? beta * *cp : 0.0f);
+    const float c = alpha * sum + (read_c ? beta * *cp : 0.0f);
+    *cp = c;
+    if (bias) out2[(uint64_t)m * ldc + n] = c + bias[n];
 }
 
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
@@ -612,7 +618,8 @@ template <bool TA, bool TB>
 __global__ void __launch_bounds__(256) k_sgemm_valu(uint32_t M, uint32_t N, uint32_t K, float alpha,
                                                     const float* __restrict__ A, uint32_t lda,
                                                     const float* __restrict__ B, uint32_t ldb, float beta,
-                                                    float* __restrict__ C, uint32_t ldc, int read_c) {
+                                                    float* __restrict__ C, uint32_t ldc, int read_c,
+                                                    const float* __restrict__ bias, float* __restrict__ out2) {
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (uint64_t)M * N) return;
     const uint32_t m = (uint32_t)(i / N), n = (uint32_t)(i % N);
@@ -624,7 +631,9 @@ __global__ void __launch_bounds__(256) k_sgemm_valu(uint32_t M, uint32_t N, uint
         sum = __builtin_fmaf(a, b, sum);
     }
     float* cp = &C[(uint64_t)m * ldc + n];
-    *cp = __builtin_fmaf(alpha, sum, read_c ? beta * *cp : 0.0f);
+    const float c = __builtin_fmaf(alpha, sum, read_c ? beta * *cp : 0.0f);
+    *cp = c;
+    if (bias) out2[(uint64_t)m * ldc + n] = c + bias[n];  // separately rounded, as src/rpl_core.c:112-120
 }
 
 constexpr uint32_t kValuMaxK = 256;
@@ -656,9 +665,12 @@ __global__ void __launch_bounds__(256) k_sgemm_valu_split(uint32_t M, uint32_t N
 
 // read_c = 0: C is written without being read (beta ignored); the result
 // equals that of read_c = 1 over C = 0 bit for bit (alpha*x + 0.0f).
+// bias (ldc == N): also out2 = C + bias[n], fused into the last pass of the
+// VALU and split-K paths, a broadcast add after the others.
 template <bool TA, bool TB>
 int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint32_t lda, const float* B,
-           uint32_t ldb, float beta, float* C, uint32_t ldc, hipStream_t s, int read_c = 1) {
+           uint32_t ldb, float beta, float* C, uint32_t ldc, hipStream_t s, int read_c = 1,
+           const float* bias = nullptr, float* out2 = nullptr) {
     // 128-bit paths need the contiguous extents and leading dimensions to be
     // multiples of 4 floats and 16-byte aligned bases.
     bool vec = aligned16(A) && aligned16(B) && aligned16(C) && lda % 4 == 0 && ldb % 4 == 0 &&
@@ -668,7 +680,7 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
     if (K > 0 && K <= kValuMaxK && (uint64_t)M * N * K <= kValuMaxWork) {
         const uint64_t blocks = ((uint64_t)M * N + 255) / 256;  // M*N <= 2^23
         hipLaunchKernelGGL((k_sgemm_valu<TA, TB>), dim3((uint32_t)blocks), dim3(256), 0, s, M, N, K, alpha, A, lda, B,
-                           ldb, beta, C, ldc, read_c);
+                           ldb, beta, C, ldc, read_c, bias, out2);
         return rplhip::check_launch("sgemm (VALU)");
     }
     if (K > kValuMaxK && (uint64_t)M * N * K <= kValuMaxWork) {
@@ -685,7 +697,7 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
         st = rplhip::check_launch("sgemm (VALU split-K)");
         if (!st) {
             hipLaunchKernelGGL(k_splitk_reduce, dim3(blocks), dim3(256), 0, s, (const float*)ws, ns, M, N, alpha, beta,
-                               C, ldc, read_c);
+                               C, ldc, read_c, bias, out2);
             st = rplhip::check_launch("sgemm (VALU split-K reduction)");
         }
         rplhip::ws_free(ws, s);
@@ -701,7 +713,8 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
         b_bytes < (1ull << 31) && !(dma_env && dma_env[0] == '0')) {
         hipLaunchKernelGGL((k_sgemm_dma<TA, TB>), dim3((uint32_t)big_tiles), dim3(fd::kThreads), 0, s, M, N, K, alpha,
                            A, lda, B, ldb, beta, C, ldc, read_c);
-        return rplhip::check_launch("sgemm (direct-to-LDS)");
+        const int st = rplhip::check_launch("sgemm (direct-to-LDS)");
+        return st || !bias ? st : rplhip_add_broadcast(C, bias, out2, (uint64_t)M * N, N, s);
     }
     const uint32_t splits = k_splits(tiles, K);
     if (splits > 1) {
@@ -724,7 +737,7 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
         if (!st) {
             const uint64_t total = (uint64_t)M * N;
             hipLaunchKernelGGL(k_splitk_reduce, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, W, ns, M, N,
-                               alpha, beta, C, ldc, read_c);
+                               alpha, beta, C, ldc, read_c, bias, out2);
             st = rplhip::check_launch("sgemm (split-K reduction)");
         }
         rplhip::ws_free(ws, s);
@@ -736,7 +749,8 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
     else
         hipLaunchKernelGGL((k_sgemm<TA, TB, false, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B,
                            ldb, beta, C, ldc, K, 0ull, 0ull, 0ull, read_c);
-    return rplhip::check_launch("sgemm");
+    const int st = rplhip::check_launch("sgemm");
+    return st || !bias ? st : rplhip_add_broadcast(C, bias, out2, (uint64_t)M * N, N, s);
 }
 
 // `batch` GEMMs of one shape in one launch of the 128 x 128 kernel (grid z =
@@ -782,6 +796,14 @@ extern "C" int rplhip_sgemm(int trans_a, int trans_b, uint32_t M, uint32_t N, ui
     if (!trans_a && trans_b) return launch<false, true>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
     if (trans_a && !trans_b) return launch<true, false>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
     return launch<true, true>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
+}
+
+extern "C" int rplhip__linear_forward(const float* X, const float* W, const float* b, float* mm, float* out,
+                                      uint32_t M, uint32_t N, uint32_t K, rplhip_stream_t stream) {
+    if (M == 0 || N == 0) return RPLHIP_OK;
+    if (!mm || !out || !b || (K && (!X || !W))) return fail(RPLHIP_ERR_INVALID, "rplhip__linear_forward: NULL pointer");
+    RPLHIP_REQUIRE_DEVICE();
+    return launch<false, true>(M, N, K, 1.0f, X, K, W, K, 0.0f, mm, N, as_stream(stream), 0, b, out);
 }
 
 extern "C" int rplhip_sgemm_batched(int trans_a, int trans_b, uint32_t M, uint32_t N, uint32_t K, float alpha,

@@ -4,6 +4,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "rplhip_internal.h"
 
 namespace {
 
@@ -42,19 +43,24 @@ __global__ void __launch_bounds__(kThreads) k_relu(const float* __restrict__ x, 
     }
 }
 
-// rpl_core.c:421
+// rpl_core.c:421.  overwrite: dx holds zeros only logically and is written
+// (0.0f + dy, or 0.0f where x <= 0), the bits of the accumulation into +0.0.
 __global__ void __launch_bounds__(kThreads) k_relu_backward(const float* __restrict__ x,
                                                             const float* __restrict__ dy,
-                                                            float* __restrict__ dx, uint64_t n) {
-    GRID_STRIDE(i, n) {
-        if (x[i] > 0) dx[i] += dy[i];
+                                                            float* __restrict__ dx, uint64_t n, int overwrite) {
+    if (overwrite) {
+        GRID_STRIDE(i, n) { dx[i] = x[i] > 0 ? 0.0f + dy[i] : 0.0f; }
+    } else {
+        GRID_STRIDE(i, n) {
+            if (x[i] > 0) dx[i] += dy[i];
+        }
     }
 }
 
-// rpl_core.c:324
+// rpl_core.c:324 (overwrite: dx = 0.0f + dy, as into a zeroed dx)
 __global__ void __launch_bounds__(kThreads) k_accumulate(const float* __restrict__ dy,
-                                                         float* __restrict__ dx, uint64_t n) {
-    GRID_STRIDE(i, n) { dx[i] += dy[i]; }
+                                                         float* __restrict__ dx, uint64_t n, int overwrite) {
+    GRID_STRIDE(i, n) { dx[i] = (overwrite ? 0.0f : dx[i]) + dy[i]; }
 }
 
 __global__ void __launch_bounds__(kThreads) k_fill(float* __restrict__ x, uint64_t n, float v) {
@@ -111,7 +117,7 @@ __global__ void __launch_bounds__(kThreads) k_colsum_partial(const float* __rest
 // flight (a chain of one load per split was latency-bound: 11.6 us for 64
 // splits), then the lane sums are added in lane order (deterministic).
 __global__ void __launch_bounds__(kThreads) k_colsum_finish(const float* __restrict__ part, int splits,
-                                                            uint64_t nb, float* __restrict__ db) {
+                                                            uint64_t nb, float* __restrict__ db, int overwrite) {
     __shared__ float red[kRowLanes][kColTile];
     const uint64_t c = (uint64_t)blockIdx.x * kColTile + threadIdx.x % kColTile;
     const int lane_r = threadIdx.x / kColTile;
@@ -132,7 +138,7 @@ __global__ void __launch_bounds__(kThreads) k_colsum_finish(const float* __restr
     if (lane_r == 0 && c < nb) {
         float t = red[0][threadIdx.x];
         for (int r = 1; r < kRowLanes; r++) t += red[r][threadIdx.x];
-        db[c] += t;
+        db[c] = (overwrite ? 0.0f : db[c]) + t;
     }
 }
 
@@ -168,14 +174,15 @@ __global__ void __launch_bounds__(kThreads) k_sqerr_finish(const float* __restri
     if (threadIdx.x == 0) loss[0] = acc / (float)n;  // rpl_core.c:457
 }
 
-// rpl_core.c:441-444
+// rpl_core.c:441-444.  The update contracts to fma(g0 * factor, p - t, dp);
+// overwrite uses +0.0 for dp, as a zeroed gradient would hold.
 __global__ void __launch_bounds__(kThreads) k_mse_backward(const float* __restrict__ p,
                                                            const float* __restrict__ t, uint64_t n,
                                                            const float* __restrict__ g0p,
-                                                           float* __restrict__ dp) {
+                                                           float* __restrict__ dp, int overwrite) {
     float factor = 2.0f / (float)n;
     float g0 = *g0p;
-    GRID_STRIDE(i, n) { dp[i] += g0 * factor * (p[i] - t[i]); }
+    GRID_STRIDE(i, n) { dp[i] = (overwrite ? 0.0f : dp[i]) + g0 * factor * (p[i] - t[i]); }
 }
 
 // Activations of the device seam (tensor_sigmoid_gpu / tensor_tanh_gpu /
@@ -270,22 +277,32 @@ int rplhip_relu(const float* x, float* y, uint64_t n, rplhip_stream_t stream) {
     return check_launch("relu");
 }
 
-int rplhip_relu_backward(const float* x, const float* dy, float* dx, uint64_t n,
-                         rplhip_stream_t stream) {
+int rplhip__relu_backward(const float* x, const float* dy, float* dx, uint64_t n, int overwrite,
+                          rplhip_stream_t stream) {
     if (n == 0) return RPLHIP_OK;
     NEED(x && dy && dx, "rplhip_relu_backward");
     RPLHIP_REQUIRE_DEVICE();
     hipLaunchKernelGGL(k_relu_backward, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), x, dy,
-                       dx, n);
+                       dx, n, overwrite);
     return check_launch("relu_backward");
 }
 
-int rplhip_accumulate(const float* dy, float* dx, uint64_t n, rplhip_stream_t stream) {
+int rplhip_relu_backward(const float* x, const float* dy, float* dx, uint64_t n,
+                         rplhip_stream_t stream) {
+    return rplhip__relu_backward(x, dy, dx, n, 0, stream);
+}
+
+int rplhip__accumulate(const float* dy, float* dx, uint64_t n, int overwrite, rplhip_stream_t stream) {
     if (n == 0) return RPLHIP_OK;
     NEED(dy && dx, "rplhip_accumulate");
     RPLHIP_REQUIRE_DEVICE();
-    hipLaunchKernelGGL(k_accumulate, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), dy, dx, n);
+    hipLaunchKernelGGL(k_accumulate, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), dy, dx, n,
+                       overwrite);
     return check_launch("accumulate");
+}
+
+int rplhip_accumulate(const float* dy, float* dx, uint64_t n, rplhip_stream_t stream) {
+    return rplhip__accumulate(dy, dx, n, 0, stream);
 }
 
 int rplhip_fill(float* x, uint64_t n, float value, rplhip_stream_t stream) {
@@ -297,6 +314,10 @@ int rplhip_fill(float* x, uint64_t n, float value, rplhip_stream_t stream) {
 }
 
 int rplhip_bias_grad(const float* dy, uint64_t n, float* db, uint64_t nb, rplhip_stream_t stream) {
+    return rplhip__bias_grad(dy, n, db, nb, 0, stream);
+}
+
+int rplhip__bias_grad(const float* dy, uint64_t n, float* db, uint64_t nb, int overwrite, rplhip_stream_t stream) {
     if (nb == 0) return RPLHIP_OK;
     NEED(dy && db, "rplhip_bias_grad");
     RPLHIP_REQUIRE_DEVICE();
@@ -321,7 +342,7 @@ int rplhip_bias_grad(const float* dy, uint64_t n, float* db, uint64_t nb, rplhip
     hipLaunchKernelGGL(k_colsum_partial, dim3((unsigned)cx, (unsigned)splits), dim3(kThreads), 0, s, dy, n,
                        full_rows, nb, rps, (float*)ws);
     hipLaunchKernelGGL(k_colsum_finish, dim3((unsigned)cx), dim3(kThreads), 0, s, (const float*)ws, (int)splits, nb,
-                       db);
+                       db, overwrite);
     st = check_launch("bias_grad");
     ws_free(ws, s);
     return st;
@@ -344,14 +365,19 @@ int rplhip_mse_loss(const float* pred, const float* target, uint64_t n, float* l
     return st;
 }
 
-int rplhip_mse_backward(const float* pred, const float* target, uint64_t n, const float* g0,
-                        float* dpred, rplhip_stream_t stream) {
+int rplhip__mse_backward(const float* pred, const float* target, uint64_t n, const float* g0, float* dpred,
+                         int overwrite, rplhip_stream_t stream) {
     if (n == 0) return RPLHIP_OK;
     NEED(pred && target && g0 && dpred, "rplhip_mse_backward");
     RPLHIP_REQUIRE_DEVICE();
     hipLaunchKernelGGL(k_mse_backward, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), pred,
-                       target, n, g0, dpred);
+                       target, n, g0, dpred, overwrite);
     return check_launch("mse_backward");
+}
+
+int rplhip_mse_backward(const float* pred, const float* target, uint64_t n, const float* g0,
+                        float* dpred, rplhip_stream_t stream) {
+    return rplhip__mse_backward(pred, target, n, g0, dpred, 0, stream);
 }
 
 static int launch_act(int act, const float* x, float* y, uint64_t n, rplhip_stream_t stream, const char* what) {

@@ -144,26 +144,37 @@ Tensor* tensor_mse_loss(const Tensor* pred, const Tensor* target) {
     return out;
 }
 
-/* src/rpl_core.c:319-337 */
+/* src/rpl_core.c:319-337.  Gradients are accumulated; a device gradient
+ * that is still zero only logically is overwritten instead (the same bits). */
 void backward_add(Tensor* t) {
     Tensor* a = t->parent1;
     Tensor* b = t->parent2;
     if (a && a->grad) {
         RplStage s = {0};
+        int ow = 0;
         const float* dy = rpl__view_grad(&s, t, 1, 0);
-        float* da = rpl__view_grad(&s, a, 1, 1);
-        if (!s.err) s.err = !rpl__ok(rplhip_accumulate(dy, da, t->size, NULL), "backward_add");
+        float* da = rpl__view_grad_acc(&s, a, &ow);
+        if (!s.err) s.err = !rpl__ok(rplhip__accumulate(dy, da, t->size, ow, NULL), "backward_add");
         rpl__stage_finish(&s);
         if (a->backward_fn) a->backward_fn(a);
     }
     if (b && b->grad) {
         RplStage s = {0};
+        int ow = 0;
         const float* dy = rpl__view_grad(&s, t, 1, 0);
-        float* db = rpl__view_grad(&s, b, 1, 1);
-        if (!s.err) s.err = !rpl__ok(rplhip_bias_grad(dy, t->size, db, b->size, NULL), "backward_add (bias)");
+        float* db = rpl__view_grad_acc(&s, b, &ow);
+        if (!s.err) s.err = !rpl__ok(rplhip__bias_grad(dy, t->size, db, b->size, ow, NULL), "backward_add (bias)");
         rpl__stage_finish(&s);
         if (b->backward_fn) b->backward_fn(b);
     }
+}
+
+/* C += op(A) op(B) (beta = 1), or C = op(A) op(B) + 0.0f when C's values
+ * are zero only logically (overwrite): the same bits, C not read. */
+static int sgemm_acc(int ta, int tb, uint32_t M, uint32_t N, uint32_t K, const float* A, uint32_t lda,
+                     const float* B, uint32_t ldb, float* C, uint32_t ldc, int overwrite) {
+    return rplhip_sgemm_batched(ta, tb, M, N, K, 1.0f, A, lda, 0, B, ldb, 0, 1.0f, C, ldc, 0, 1, overwrite ? 0 : 1,
+                                NULL);
 }
 
 /* src/rpl_core.c:363-416, including its layout guess for B (b is taken as
@@ -176,26 +187,28 @@ void backward_matmul(Tensor* t) {
     if (a->grad) {
         /* dA[M,K] += dt[M,N] * (b_trans ? B[N,K] : B[K,N]^T) */
         RplStage s = {0};
+        int ow = 0;
         const float* dt = rpl__view_grad(&s, t, 1, 0);
         const float* db = rpl__view_data(&s, b, 1, 0);
-        float* da = rpl__view_grad(&s, a, 1, 1);
+        float* da = rpl__view_grad_acc(&s, a, &ow);
         if (!s.err)
-            s.err = !rpl__ok(rplhip_sgemm(0, !b_trans, M, K, N, 1.0f, dt, N, db, b_trans ? K : N, 1.0f, da, K, NULL),
+            s.err = !rpl__ok(sgemm_acc(0, !b_trans, M, K, N, dt, N, db, b_trans ? K : N, da, K, ow),
                              "backward_matmul (dA)");
         rpl__stage_finish(&s);
         if (a->backward_fn) a->backward_fn(a);
     }
     if (b->grad) {
         RplStage s = {0};
+        int ow = 0;
         const float* dt = rpl__view_grad(&s, t, 1, 0);
         const float* da = rpl__view_data(&s, a, 1, 0);
-        float* dbg = rpl__view_grad(&s, b, 1, 1);
+        float* dbg = rpl__view_grad_acc(&s, b, &ow);
         int st = RPLHIP_OK;
         if (!s.err) {
             if (b_trans) /* dB[N,K] += dt^T[N,M] * A[M,K] */
-                st = rplhip_sgemm(1, 0, N, K, M, 1.0f, dt, N, da, K, 1.0f, dbg, K, NULL);
+                st = sgemm_acc(1, 0, N, K, M, dt, N, da, K, dbg, K, ow);
             else /* dB[K,N] += A^T[K,M] * dt[M,N] */
-                st = rplhip_sgemm(1, 0, K, N, M, 1.0f, da, K, dt, N, 1.0f, dbg, N, NULL);
+                st = sgemm_acc(1, 0, K, N, M, da, K, dt, N, dbg, N, ow);
             s.err = !rpl__ok(st, "backward_matmul (dB)");
         }
         rpl__stage_finish(&s);
@@ -208,10 +221,11 @@ void backward_relu(Tensor* t) {
     Tensor* a = t->parent1;
     if (a && a->grad) {
         RplStage s = {0};
+        int ow = 0;
         const float* dx = rpl__view_data(&s, a, 1, 0);
         const float* dy = rpl__view_grad(&s, t, 1, 0);
-        float* dg = rpl__view_grad(&s, a, 1, 1);
-        if (!s.err) s.err = !rpl__ok(rplhip_relu_backward(dx, dy, dg, t->size, NULL), "backward_relu");
+        float* dg = rpl__view_grad_acc(&s, a, &ow);
+        if (!s.err) s.err = !rpl__ok(rplhip__relu_backward(dx, dy, dg, t->size, ow, NULL), "backward_relu");
         rpl__stage_finish(&s);
         if (a->backward_fn) a->backward_fn(a);
     }
@@ -223,12 +237,13 @@ void backward_mse(Tensor* t) {
     Tensor* target = t->parent2;
     if (pred && pred->grad) {
         RplStage s = {0};
+        int ow = 0;
         const float* dp = rpl__view_data(&s, pred, 1, 0);
         const float* dtg = rpl__view_data(&s, target, 1, 0);
         const float* g0 = rpl__view_grad(&s, t, 1, 0);
-        float* dg = rpl__view_grad(&s, pred, 1, 1);
+        float* dg = rpl__view_grad_acc(&s, pred, &ow);
         if (!s.err)
-            s.err = !rpl__ok(rplhip_mse_backward(dp, dtg, pred->size, g0, dg, NULL), "backward_mse");
+            s.err = !rpl__ok(rplhip__mse_backward(dp, dtg, pred->size, g0, dg, ow, NULL), "backward_mse");
         rpl__stage_finish(&s);
         if (pred->backward_fn) pred->backward_fn(pred);
     }
@@ -244,17 +259,17 @@ void tensor_backward(Tensor* t) {
     for (uint32_t i = 0; i < t->size; i++) t->grad[i] = 1.0f;
     if (rpl__is_gpu(t)) {
         if (!rpl__attach_grad(t)) return;
+        rpl__grad_take_zero(t); /* overwritten by the fill */
         if (!rpl__ok(rplhip_fill(rpl__dev_grad(t), t->size, 1.0f, NULL), "tensor_backward")) return;
     }
     if (t->backward_fn) t->backward_fn(t);
 }
 
-/* src/rpl_core.c:478-480 */
+/* src/rpl_core.c:478-480 (the device gradient is marked zero, not written) */
 void tensor_zero_grad(Tensor* t) {
     if (!t || !t->grad) return;
     memset(t->grad, 0, (size_t)t->size * sizeof(float));
-    float* g = rpl__dev_grad(t);
-    if (g) rpl__ok(rplhip_memset(g, 0, (size_t)t->size * sizeof(float), NULL), "tensor_zero_grad");
+    rpl__grad_set_zero(t);
 }
 
 /* src/rpl_nn.c:23-43: same Xavier-style init from rand(), so a given
@@ -290,7 +305,12 @@ Tensor* linear_forward(Linear* layer, const Tensor* input) {
      * the fill; otherwise zero the buffer (on the device when resident: its
      * host copy is stale by definition) and go through tensor_gemm. */
     const uint32_t M = input->shape[0], K = input->shape[1], N = layer->out_features;
-    if (gpu && rpl__is_gpu(input) && rpl__is_gpu(layer->weight) && input->dims == 2 && K == layer->in_features) {
+    const int fused = gpu && rpl__is_gpu(input) && rpl__is_gpu(layer->weight) && rpl__is_gpu(layer->bias) &&
+                      input->dims == 2 && K == layer->in_features && layer->bias->size == N;
+    if (fused) {
+        /* GEMM and bias add in one call (the add fused into the GEMM's last
+         * pass where its path allows); out's graph links are set below. */
+    } else if (gpu && rpl__is_gpu(input) && rpl__is_gpu(layer->weight) && input->dims == 2 && K == layer->in_features) {
         rpl__ok(rplhip_sgemm_batched(0, 1, M, N, K, 1.0f, rpl__dev_data(input), K, 0, rpl__dev_data(layer->weight),
                                      K, 0, 0.0f, rpl__dev_data(matmul_out), N, 0, 1, 0, NULL),
                 "linear_forward");
@@ -310,7 +330,19 @@ Tensor* linear_forward(Linear* layer, const Tensor* input) {
     Tensor* out = create(2, output_shape, matmul_out->requires_grad || layer->bias->requires_grad);
     if (!out) return NULL;
     if (gpu && !rpl__attach(out, 0)) return NULL;
-    tensor_add_out(out, matmul_out, layer->bias);
+    if (fused) {
+        rpl__ok(rplhip__linear_forward(rpl__dev_data(input), rpl__dev_data(layer->weight), rpl__dev_data(layer->bias),
+                                       rpl__dev_data(matmul_out), rpl__dev_data(out), M, N, K, NULL),
+                "linear_forward");
+        if (out->requires_grad) { /* tensor_add_out's graph links (src/rpl_core.c:122-128) */
+            out->parent1 = matmul_out;
+            out->parent2 = layer->bias;
+            out->backward_fn = backward_add;
+            out->is_leaf = false;
+        }
+    } else {
+        tensor_add_out(out, matmul_out, layer->bias);
+    }
     if (gpu) rpl__adopt(out, matmul_out);
     return out;
 }

@@ -48,9 +48,10 @@ void backward_fake_quant(Tensor* t) {
     Tensor* input = t->parent1;
     if (input && input->grad) {
         RplStage s = {0};
+        int ow = 0;
         const float* dy = rpl__view_grad(&s, t, 1, 0);
-        float* dx = rpl__view_grad(&s, input, 1, 1);
-        if (!s.err) s.err = !rpl__ok(rplhip_accumulate(dy, dx, t->size, NULL), "backward_fake_quant");
+        float* dx = rpl__view_grad_acc(&s, input, &ow);
+        if (!s.err) s.err = !rpl__ok(rplhip__accumulate(dy, dx, t->size, ow, NULL), "backward_fake_quant");
         rpl__stage_finish(&s);
         if (input->backward_fn) input->backward_fn(input);
     }

@@ -7,6 +7,7 @@
 
 #include "rpl.h"
 #include "rplhip.h"
+#include "rplhip_internal.h"
 
 /* Record a failure of `what` (prints it, sets rpl_last_error) when st != 0.
  * Returns 1 on success, 0 on failure. */
@@ -39,6 +40,16 @@ int rpl__is_gpu(const Tensor* t);
  * root whose host gradient was created after it went to the device). */
 int rpl__attach_grad(Tensor* t);
 
+/* Device gradients are zeroed lazily: a new output's gradient, one attached
+ * by rpl__attach_grad and one cleared by tensor_zero_grad are only marked
+ * zero.  The first accumulation into a marked gradient overwrites it
+ * (0 + x, the same bits as accumulating into zeros); readers get it filled.
+ * rpl__grad_take_zero tests and clears the mark, rpl__grad_set_zero sets it,
+ * rpl__dev_grad_ready fills a marked gradient and returns it. */
+int rpl__grad_take_zero(const Tensor* t);
+void rpl__grad_set_zero(const Tensor* t);
+float* rpl__dev_grad_ready(const Tensor* t);
+
 /* Staging of host tensors through device memory for one call. */
 #define RPL_STAGE_MAX 12
 typedef struct {
@@ -58,6 +69,11 @@ typedef struct {
 void* rpl__stage_host(RplStage* s, void* host, size_t bytes, int upload, int writeback);
 float* rpl__view_data(RplStage* s, const Tensor* t, int upload, int writeback);
 float* rpl__view_grad(RplStage* s, const Tensor* t, int upload, int writeback);
+/* The gradient of t as the target of an accumulation (grad += x): staged
+ * with write-back for host tensors; for GPU-resident ones the device
+ * gradient, with *overwrite = 1 when it was zero only logically (the caller
+ * must then write every element, as 0 + x). */
+float* rpl__view_grad_acc(RplStage* s, const Tensor* t, int* overwrite);
 /* Copies write-backs to the host (synchronizing if there are any), releases
  * the staging buffers.  Returns 1 if the call succeeded. */
 int rpl__stage_finish(RplStage* s);

@@ -114,6 +114,7 @@ typedef struct {
     float* grad;
     size_t bytes;
     int used;
+    int grad_zero; /* the device gradient is zero, not yet written (contents undefined) */
 } RegEntry;
 
 enum { kRegChunkBits = 10, kRegChunk = 1 << kRegChunkBits, kRegMaxChunks = 4096 };
@@ -139,7 +140,7 @@ static int reg_read(uint32_t h, RegEntry* out) {
     return e != NULL;
 }
 
-static uint32_t reg_new(float* data, float* grad, size_t bytes) {
+static uint32_t reg_new(float* data, float* grad, size_t bytes, int grad_zero) {
     pthread_mutex_lock(&g_reg_mu);
     uint32_t h = 0;
     for (uint32_t i = 0; i < g_reg_len; i++)
@@ -167,6 +168,7 @@ static uint32_t reg_new(float* data, float* grad, size_t bytes) {
     e->grad = grad;
     e->bytes = bytes;
     e->used = 1;
+    e->grad_zero = grad_zero;
     pthread_mutex_unlock(&g_reg_mu);
     return h;
 }
@@ -220,10 +222,9 @@ int rpl__attach(Tensor* t, int upload) {
     if (!d) return 0;
     float* g = NULL;
     if (t->grad) {
+        /* A new output's gradient starts as zero: recorded, not written. */
         g = (float*)rpl__pool_alloc(bytes);
-        if (!g || !rpl__ok(upload ? rplhip_memcpy_htod(g, t->grad, bytes)
-                                  : rplhip_memset(g, 0, bytes, NULL),
-                           "tensor grad to device")) {
+        if (!g || (upload && !rpl__ok(rplhip_memcpy_htod(g, t->grad, bytes), "tensor grad to device"))) {
             rpl__pool_free(d, bytes);
             if (g) rpl__pool_free(g, bytes);
             return 0;
@@ -234,7 +235,7 @@ int rpl__attach(Tensor* t, int upload) {
         if (g) rpl__pool_free(g, bytes);
         return 0;
     }
-    uint32_t h = reg_new(d, g, bytes);
+    uint32_t h = reg_new(d, g, bytes, g && !upload);
     if (!h) {
         rpl__pool_free(d, bytes);
         if (g) rpl__pool_free(g, bytes);
@@ -251,12 +252,9 @@ int rpl__attach_grad(Tensor* t) {
     if (e.grad) return 1;
     float* g = (float*)rpl__pool_alloc(e.bytes);
     if (!g) return 0;
-    if (!rpl__ok(rplhip_memset(g, 0, e.bytes, NULL), "device gradient")) {
-        rpl__pool_free(g, e.bytes);
-        return 0;
-    }
-    /* Install by handle under the lock; if another thread installed one (or
-     * released the tensor) meanwhile, keep the table as it is. */
+    /* Install by handle under the lock (as zero, not yet written); if another
+     * thread installed one (or released the tensor) meanwhile, keep the
+     * table as it is. */
     int installed = 0, live = 0;
     pthread_mutex_lock(&g_reg_mu);
     RegEntry* s = reg_slot(t->gpu_buffer);
@@ -264,12 +262,47 @@ int rpl__attach_grad(Tensor* t) {
         live = 1;
         if (!s->grad) {
             s->grad = g;
+            s->grad_zero = 1;
             installed = 1;
         }
     }
     pthread_mutex_unlock(&g_reg_mu);
     if (!installed) rpl__pool_free(g, e.bytes);
     return live;
+}
+
+/* Test and clear the zero mark of t's device gradient: 1 if it was zero
+ * only logically -- the caller then writes every element (as 0 + x). */
+int rpl__grad_take_zero(const Tensor* t) {
+    if (!t || t->device != DEVICE_GPU) return 0;
+    int was = 0;
+    pthread_mutex_lock(&g_reg_mu);
+    RegEntry* e = reg_slot(t->gpu_buffer);
+    if (e && e->grad && e->grad_zero) {
+        was = 1;
+        e->grad_zero = 0;
+    }
+    pthread_mutex_unlock(&g_reg_mu);
+    return was;
+}
+
+/* Mark t's device gradient zero without writing it (tensor_zero_grad). */
+void rpl__grad_set_zero(const Tensor* t) {
+    if (!t || t->device != DEVICE_GPU) return;
+    pthread_mutex_lock(&g_reg_mu);
+    RegEntry* e = reg_slot(t->gpu_buffer);
+    if (e && e->grad) e->grad_zero = 1;
+    pthread_mutex_unlock(&g_reg_mu);
+}
+
+/* t's device gradient with its values in memory: a zero-marked gradient is
+ * filled with zeros first.  NULL if t has none. */
+float* rpl__dev_grad_ready(const Tensor* t) {
+    float* g = rpl__dev_grad(t);
+    if (g && rpl__grad_take_zero(t) &&
+        !rpl__ok(rplhip_fill(g, t->size, 0.0f, NULL), "device gradient"))
+        return NULL;
+    return g;
 }
 
 /* ---------------------------------------------------------------- staging */
@@ -309,7 +342,7 @@ float* rpl__view_data(RplStage* s, const Tensor* t, int upload, int writeback) {
 float* rpl__view_grad(RplStage* s, const Tensor* t, int upload, int writeback) {
     if (s->err) return NULL;
     if (rpl__is_gpu(t)) {
-        float* g = rpl__dev_grad(t);
+        float* g = rpl__dev_grad_ready(t);
         if (!g) {
             s->err = 1;
             rpl__bad("autograd", "GPU tensor has no device gradient");
@@ -317,6 +350,22 @@ float* rpl__view_grad(RplStage* s, const Tensor* t, int upload, int writeback) {
         return g;
     }
     return (float*)rpl__stage_host(s, t->grad, (size_t)t->size * sizeof(float), upload, writeback);
+}
+
+float* rpl__view_grad_acc(RplStage* s, const Tensor* t, int* overwrite) {
+    *overwrite = 0;
+    if (s->err) return NULL;
+    if (rpl__is_gpu(t)) {
+        float* g = rpl__dev_grad(t);
+        if (!g) {
+            s->err = 1;
+            rpl__bad("autograd", "GPU tensor has no device gradient");
+            return NULL;
+        }
+        *overwrite = rpl__grad_take_zero(t);
+        return g;
+    }
+    return (float*)rpl__stage_host(s, t->grad, (size_t)t->size * sizeof(float), 1, 1);
 }
 
 int rpl__stage_finish(RplStage* s) {
@@ -475,7 +524,7 @@ void rpl_gpu_synchronize(void) { rpl__ok(rplhip_synchronize(), "rpl_gpu_synchron
 void* rpl_gpu_stream(void) { return NULL; }
 
 float* rpl_tensor_device_data(const Tensor* t) { return rpl__dev_data(t); }
-float* rpl_tensor_device_grad(const Tensor* t) { return rpl__dev_grad(t); }
+float* rpl_tensor_device_grad(const Tensor* t) { return rpl__dev_grad_ready(t); }
 
 /* src/rpl_gpu.c:201-214: upload and mark GPU-resident (no-op if already). */
 void tensor_to_gpu(Tensor* t) {
@@ -493,5 +542,13 @@ void tensor_from_gpu(Tensor* t) {
     size_t bytes = (size_t)t->size * sizeof(float);
     if (!rpl__ok(rplhip_memcpy_dtoh(t->data, d, bytes), "tensor_from_gpu")) return;
     float* g = rpl__dev_grad(t);
-    if (g && t->grad) rpl__ok(rplhip_memcpy_dtoh(t->grad, g, bytes), "tensor_from_gpu (grad)");
+    if (!g || !t->grad) return;
+    if (rpl__grad_take_zero(t)) {
+        /* zero only logically: the host copy gets the zeros, the device
+         * gradient keeps its mark */
+        memset(t->grad, 0, bytes);
+        rpl__grad_set_zero(t);
+        return;
+    }
+    rpl__ok(rplhip_memcpy_dtoh(t->grad, g, bytes), "tensor_from_gpu (grad)");
 }

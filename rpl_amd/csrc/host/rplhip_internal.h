@@ -1,0 +1,39 @@
+/*
+ * Device entry points used only by the host layer (not installed, not part of
+ * include/).  Each is the include/rplhip.h function of the same name without
+ * the leading underscore plus an `overwrite` flag: when it is set, the
+ * accumulation target is taken to hold zeros and is written, not read --
+ * every element becomes 0.0f + x (or the fused form the public function
+ * applies to a target of +0.0), the same bits as accumulating into a
+ * zero-filled buffer.  The autograd layer uses them for gradients that are
+ * zero only logically (never materialized).
+ */
+#ifndef RPLHIP_INTERNAL_H
+#define RPLHIP_INTERNAL_H
+
+#include "rplhip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int rplhip__accumulate(const float* dy, float* dx, uint64_t n, int overwrite, rplhip_stream_t stream);
+int rplhip__relu_backward(const float* x, const float* dy, float* dx, uint64_t n, int overwrite,
+                          rplhip_stream_t stream);
+int rplhip__mse_backward(const float* pred, const float* target, uint64_t n, const float* g0, float* dpred,
+                         int overwrite, rplhip_stream_t stream);
+int rplhip__bias_grad(const float* dy, uint64_t n, float* db, uint64_t nb, int overwrite, rplhip_stream_t stream);
+
+/* linear_forward (src/rpl_nn.c:55-77) in one call: mm = X W^T (X [M,K],
+ * W [N,K]; C written without being read, i.e. 1.0f * sum + 0.0f as
+ * tensor_gemm over a zeroed C) and out = mm + b[n] (tensor_add_out's
+ * broadcast, src/rpl_core.c:112-120), the bias add fused into the GEMM's
+ * last pass where the GEMM path allows it.  mm may be NULL. */
+int rplhip__linear_forward(const float* X, const float* W, const float* b, float* mm, float* out, uint32_t M,
+                           uint32_t N, uint32_t K, rplhip_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -146,6 +146,76 @@ def test_config2_mlp_step(gpu, orc):
     check_mlp(orc, r, X, Y, W1, b1, W2, b2)
 
 
+def test_gradient_accumulation_and_zero_grad(gpu):
+    """Device gradients are zeroed lazily (marked, then overwritten by the
+    first accumulation).  Two backward passes without tensor_zero_grad add
+    up -- exactly twice the first pass's gradients, since both passes compute
+    the same values and doubling is exact -- and after tensor_zero_grad both
+    tensor_from_gpu and rpl_tensor_device_grad see zeros, and a further pass
+    equals the first bit for bit."""
+    lib = gpu
+    B, IN, H, O = 256, 96, 64, 10
+    rng = np.random.default_rng(21)
+    X = rng.uniform(0, 1, (B, IN)).astype(np.float32)
+    Y = np.eye(O, dtype=np.float32)[rng.integers(0, O, B)]
+    l1, l2 = lib.linear_create(IN, H), lib.linear_create(H, O)
+    for layer in (l1, l2):
+        lib.tensor_to_gpu(layer.contents.weight)
+        lib.tensor_to_gpu(layer.contents.bias)
+    tX, tY = tensor_from(lib, X), tensor_from(lib, Y)
+    lib.tensor_to_gpu(tX)
+    lib.tensor_to_gpu(tY)
+    params = (l1.contents.weight, l1.contents.bias, l2.contents.weight, l2.contents.bias)
+    shapes = ((H, IN), (H,), (O, H), (O,))
+
+    def step():
+        h = lib.linear_forward(l1, tX)
+        a = lib.tensor_relu(h)
+        o = lib.linear_forward(l2, a)
+        loss = lib.tensor_mse_loss(o, tY)
+        lib.tensor_backward(loss)
+        for t in (loss, o, a, h):
+            lib.tensor_free(t)
+
+    def grads():
+        out = []
+        for t, shp in zip(params, shapes):
+            lib.tensor_from_gpu(t)
+            out.append(host(t, shp, grad=True))
+        return out
+
+    say("gradient accumulation: zero_grad, one pass")
+    for t in params:
+        lib.tensor_zero_grad(t)
+    step()
+    g1 = grads()
+    say("gradient accumulation: second pass without zero_grad")
+    step()
+    g2 = grads()
+    for a, b in zip(g1, g2):
+        assert bits_equal(b, a * np.float32(2))
+    say("gradient accumulation: zero_grad, reads")
+    for t in params:
+        lib.tensor_zero_grad(t)
+    for t, shp in zip(params, shapes):
+        t.contents.grad[0] = 7.0  # stale host value must be replaced by the device's zeros
+        lib.tensor_from_gpu(t)
+        assert not host(t, shp, grad=True).any()
+        dg = lib.rpl_tensor_device_grad(t)
+        buf = np.full(int(np.prod(shp)), 5.0, np.float32)
+        rpl_amd.check(lib.rplhip_memcpy_dtoh(buf.ctypes.data, dg, buf.nbytes))
+        assert not buf.any()
+    say("gradient accumulation: pass after zero_grad")
+    step()
+    for a, b in zip(g1, grads()):
+        assert bits_equal(b, a)
+    assert not lib.rpl_last_error()
+    lib.tensor_free(tX)
+    lib.tensor_free(tY)
+    lib.linear_free(l1)
+    lib.linear_free(l2)
+
+
 def test_backward_matmul_layout_guess(gpu, golden):
     lib = gpu
     tA, tB = tensor_from(lib, golden["bmm_A"], True), tensor_from(lib, golden["bmm_B"], True)
