@@ -196,12 +196,104 @@ __global__ void __launch_bounds__(kThreads) k_dequantize(const int8_t* __restric
     for (uint64_t i = n4 * 4 + tid; i < n; i += stride) y[i] = (float)((int32_t)q[i] - zp) * scale;
 }
 
-// Per-channel (per-row) symmetric quantization, one block per slice:
-// min/max over the slice, scale = fmaxf(|min|,|max|)/127, then quantize.
-// Slices of up to kRegItems*4*kThreads floats with 16-byte aligned rows are
-// held in registers, so the slice is read from HBM once.
-constexpr int kRegItems = 8;  // float4 per thread -> 8192 floats per slice
-template <bool REG>
+// Per-channel (per-row) symmetric quantization: min/max over the slice,
+// scale = fmaxf(|min|,|max|)/127, then quantize (src/rpl_quantization.c:
+// 120-160).  The reference scans with `x < min` / `x > max` from FLT_MAX /
+// -FLT_MAX, so NaN is never taken and fmaxf(|min|,|max|) is the largest |x|
+// over the slice's non-NaN elements, or FLT_MAX when it has none; the
+// kernels compute that directly, in any order.
+//
+// Division by a row's scale s: when 2^-100 <= s <= 2^125, q = x * inv with
+// inv = 1.0f / s correctly rounded, then one FMA correction
+// q' = fma(fma(-q, s, x), inv, q).  For |x| >= s/4 the residual x - q*s is
+// a multiple of 2^-148, hence exact, and q' is x / s correctly rounded
+// (Markstein's theorem: inv within half an ulp of 1/s, q within an ulp of
+// x/s); below s/4 q' may differ from x / s in its last bits, but both are
+// below 1/2 in magnitude and quantize to 0.  3 VALU operations instead of
+// the ~10 of a general IEEE divide.  Other scales (0 for an all-zero slice,
+// inf, tiny or huge) divide exactly.  Checked against x / s on the CPU
+// (tests/quant_div_identity.c).
+__device__ __forceinline__ float div_scale_fast(float x, float s, float inv) {
+#pragma clang fp contract(off)
+    const float q = x * inv;
+    return __builtin_fmaf(__builtin_fmaf(-q, s, x), inv, q);
+}
+__device__ __forceinline__ bool scale_fast_ok(float s) { return s >= 0x1p-100f && s <= 0x1p125f; }
+
+// clamp(x86((int32)roundf(y)), -128, 127) as a byte.
+__device__ __forceinline__ uint32_t q8_of(float y) {
+    const int32_t v = x86_round_cvt(y);
+    return (uint8_t)(int8_t)(v < -128 ? -128 : (v > 127 ? 127 : v));
+}
+// The same for |y| < 2^31 or NaN (the quotients of the fast division are
+// at most 128 in magnitude): roundf(y) = trunc(y + copysign(0.49999997, y)),
+// clamped before the truncating conversion; fmaxf takes -128 for a NaN,
+// which is where x86's INT32_MIN clamps.  5 VALU operations.
+__device__ __forceinline__ uint32_t q8_small(float y) {
+#pragma clang fp contract(off)
+    const float t = y + __builtin_copysignf(0.49999997f, y);
+    return (uint32_t)(int32_t)__builtin_fminf(__builtin_fmaxf(t, -128.0f), 127.0f);
+}
+// Low bytes of four words packed into one (v_perm_b32).
+__device__ __forceinline__ uint32_t pack4(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+    return __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u) | __builtin_amdgcn_perm(b3, b2, 0x04000c0cu);
+}
+
+// k_quantize_rows_wave: one wave per slice of up to 256*NV floats (cols % 4
+// == 0, 16-byte aligned rows), 4 slices per block.  Lane l holds float4
+// items l, l+64, .. in registers, so the slice is read from HBM once; every
+// load is unconditional (items past the slice re-read its last float4, which
+// leaves the largest |x| unchanged) so all NV loads are in flight together,
+// and the reduction is wave-local (no LDS, no block barrier).  FULL: the
+// slice is exactly 256*NV floats (no item is past it).
+template <int NV, bool FULL>
+__global__ void __launch_bounds__(kThreads) k_quantize_rows_wave(const float* __restrict__ x, uint32_t rows,
+                                                                 uint32_t cols, int8_t* __restrict__ q,
+                                                                 float* __restrict__ scales) {
+    const uint32_t r = blockIdx.x * (kThreads / 64) + threadIdx.x / 64;
+    if (r >= rows) return;
+    const uint32_t lane = threadIdx.x % 64, n4 = cols / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(x + (uint64_t)r * cols);
+    float4 v[NV];
+#pragma unroll
+    for (int it = 0; it < NV; it++) {
+        const uint32_t i = lane + 64 * it;
+        v[it] = x4[FULL || i < n4 ? i : n4 - 1];
+    }
+    // Largest |x| over non-NaN elements (fmaxf returns the other operand
+    // for a NaN); -1 when there is none.
+    float amax = -1.0f;
+#pragma unroll
+    for (int it = 0; it < NV; it++) {
+        amax = __builtin_fmaxf(amax, __builtin_fmaxf(__builtin_fabsf(v[it].x), __builtin_fabsf(v[it].y)));
+        amax = __builtin_fmaxf(amax, __builtin_fmaxf(__builtin_fabsf(v[it].z), __builtin_fabsf(v[it].w)));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = __builtin_fmaxf(__shfl_xor(amax, off), amax);
+    const float scale = (amax < 0.0f ? FLT_MAX : amax) / 127.0f;
+    if (lane == 0) scales[r] = scale;
+    uint32_t* q4 = reinterpret_cast<uint32_t*>(q + (uint64_t)r * cols);
+    const bool fast = scale_fast_ok(scale);  // wave-uniform
+    const float inv = 1.0f / scale;
+#pragma unroll
+    for (int it = 0; it < NV; it++) {
+        const uint32_t i = lane + 64 * it;
+        if (FULL || i < n4) {
+            const float4 t = v[it];
+            uint32_t w;
+            if (fast)
+                w = pack4(q8_small(div_scale_fast(t.x, scale, inv)), q8_small(div_scale_fast(t.y, scale, inv)),
+                          q8_small(div_scale_fast(t.z, scale, inv)), q8_small(div_scale_fast(t.w, scale, inv)));
+            else
+                w = pack4(q8_of(t.x / scale), q8_of(t.y / scale), q8_of(t.z / scale), q8_of(t.w / scale));
+            q4[i] = w;
+        }
+    }
+}
+constexpr uint32_t kRowsWaveMaxCols = 256 * 32;
+
+// Other slices (cols % 4 != 0, unaligned rows, or more than
+// kRowsWaveMaxCols floats): one block per slice, read twice.
 __global__ void __launch_bounds__(kThreads) k_quantize_rows(const float* __restrict__ x, uint32_t rows,
                                                             uint32_t cols, int8_t* __restrict__ q,
                                                             float* __restrict__ scales) {
@@ -209,46 +301,14 @@ __global__ void __launch_bounds__(kThreads) k_quantize_rows(const float* __restr
     const float* xr = x + (uint64_t)r * cols;
     int8_t* qr = q + (uint64_t)r * cols;
     float mn = FLT_MAX, mx = -FLT_MAX;
-    if (REG) {
-        float4 v[kRegItems];
-        const float4* x4 = reinterpret_cast<const float4*>(xr);
-        uint32_t n4 = cols / 4;
-#pragma unroll
-        for (int it = 0; it < kRegItems; it++) {
-            uint32_t i = threadIdx.x + it * kThreads;
-            if (i < n4) {
-                v[it] = x4[i];
-                mn = sel_min(v[it].x, mn); mx = sel_max(v[it].x, mx);
-                mn = sel_min(v[it].y, mn); mx = sel_max(v[it].y, mx);
-                mn = sel_min(v[it].z, mn); mx = sel_max(v[it].z, mx);
-                mn = sel_min(v[it].w, mn); mx = sel_max(v[it].w, mx);
-            }
-        }
-        block_min_max(mn, mx);
-        float scale = fmaxf(fabsf(mn), fabsf(mx)) / 127.0f;
-        if (threadIdx.x == 0) scales[r] = scale;
-        uint32_t* q4 = reinterpret_cast<uint32_t*>(qr);
-#pragma unroll
-        for (int it = 0; it < kRegItems; it++) {
-            uint32_t i = threadIdx.x + it * kThreads;
-            if (i < n4) {
-                uint32_t b0 = (uint8_t)quantize_one(v[it].x, scale, 0);
-                uint32_t b1 = (uint8_t)quantize_one(v[it].y, scale, 0);
-                uint32_t b2 = (uint8_t)quantize_one(v[it].z, scale, 0);
-                uint32_t b3 = (uint8_t)quantize_one(v[it].w, scale, 0);
-                q4[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-            }
-        }
-    } else {
-        for (uint32_t i = threadIdx.x; i < cols; i += kThreads) {
-            mn = sel_min(xr[i], mn);
-            mx = sel_max(xr[i], mx);
-        }
-        block_min_max(mn, mx);
-        float scale = fmaxf(fabsf(mn), fabsf(mx)) / 127.0f;
-        if (threadIdx.x == 0) scales[r] = scale;
-        for (uint32_t i = threadIdx.x; i < cols; i += kThreads) qr[i] = quantize_one(xr[i], scale, 0);
+    for (uint32_t i = threadIdx.x; i < cols; i += kThreads) {
+        mn = sel_min(xr[i], mn);
+        mx = sel_max(xr[i], mx);
     }
+    block_min_max(mn, mx);
+    float scale = fmaxf(fabsf(mn), fabsf(mx)) / 127.0f;
+    if (threadIdx.x == 0) scales[r] = scale;
+    for (uint32_t i = threadIdx.x; i < cols; i += kThreads) qr[i] = quantize_one(xr[i], scale, 0);
 }
 
 // tensor_get_min_max: first index attaining the extreme wins.
@@ -401,14 +461,37 @@ int rplhip_quantize_per_channel(const float* x, uint32_t num_channels, uint32_t 
     if (!x || !q || !scales) return fail(RPLHIP_ERR_INVALID, "rplhip_quantize_per_channel: NULL pointer");
     RPLHIP_REQUIRE_DEVICE();
     hipStream_t s = as_stream(stream);
-    bool reg = channel_size % 4 == 0 && channel_size <= (uint32_t)(kRegItems * 4 * kThreads) &&
-               (((uintptr_t)x) & 15) == 0 && (((uintptr_t)q) & 3) == 0;
-    if (reg)
-        hipLaunchKernelGGL(k_quantize_rows<true>, dim3(num_channels), dim3(kThreads), 0, s, x,
-                           num_channels, channel_size, q, scales);
-    else
-        hipLaunchKernelGGL(k_quantize_rows<false>, dim3(num_channels), dim3(kThreads), 0, s, x,
-                           num_channels, channel_size, q, scales);
+    const bool reg = channel_size > 0 && channel_size % 4 == 0 && channel_size <= kRowsWaveMaxCols && (((uintptr_t)x) & 15) == 0 &&
+                     (((uintptr_t)q) & 3) == 0;
+    if (reg) {
+        const dim3 grid((num_channels + kThreads / 64 - 1) / (kThreads / 64));
+        const uint32_t nv = (channel_size + 255) / 256;
+#define RPL_QR(NV)                                                                                         \
+    do {                                                                                                   \
+        if (channel_size == 256 * NV)                                                                      \
+            hipLaunchKernelGGL((k_quantize_rows_wave<NV, true>), grid, dim3(kThreads), 0, s, x, num_channels, \
+                               channel_size, q, scales);                                                   \
+        else                                                                                               \
+            hipLaunchKernelGGL((k_quantize_rows_wave<NV, false>), grid, dim3(kThreads), 0, s, x,            \
+                               num_channels, channel_size, q, scales);                                     \
+    } while (0)
+        if (nv <= 1)
+            RPL_QR(1);
+        else if (nv <= 2)
+            RPL_QR(2);
+        else if (nv <= 4)
+            RPL_QR(4);
+        else if (nv <= 8)
+            RPL_QR(8);
+        else if (nv <= 16)
+            RPL_QR(16);
+        else
+            RPL_QR(32);
+#undef RPL_QR
+    } else {
+        hipLaunchKernelGGL(k_quantize_rows, dim3(num_channels), dim3(kThreads), 0, s, x, num_channels, channel_size,
+                           q, scales);
+    }
     return check_launch("quantize_per_channel");
 }
 

@@ -158,11 +158,15 @@ def test_quantize_unaligned_pointers(gpu, orc):
 
 
 # Rows of up to 8192 floats with cols % 4 == 0 and aligned rows are held in
-# registers (k_quantize_rows<true>: whole and partial 1024-float passes of
-# the block), others are read twice (k_quantize_rows<false>: 33 x 1001,
-# 3 x 9000, odd row starts).
+# registers, one wave per row (k_quantize_rows_wave<NV>, 256*NV floats per
+# wave: NV = 1 for 4..256 columns, 2 up to 512, 4 up to 1024, 8 up to 2048,
+# 16 up to 4096, 32 up to 8192; row counts that are not a multiple of the
+# block's 4 rows); others are read twice, one block per row
+# (k_quantize_rows: 33 x 1001, 3 x 9000, odd row starts).
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (8192, 8192), (33, 1001), (3, 9000), (1, 64), (2048, 4096),
-                                       (7, 4112), (5, 16), (9, 1004), (6, 8192), (13, 2060), (3, 4)])
+                                       (7, 4112), (5, 16), (9, 1004), (6, 8192), (13, 2060), (3, 4),
+                                       (11, 260), (6, 512), (10, 1024), (5, 1500), (3, 2048), (2, 3000),
+                                       (17, 252)])
 def test_per_channel_vs_oracle(gpu, orc, rows, cols):
     x = rpl_amd.fill_normal(rows * cols, seed(94, 7)).reshape(rows, cols)
     say("per-channel", rows, cols)
@@ -192,6 +196,17 @@ def test_per_channel_special_rows(gpu, orc, cols):
     q, s = dev_per_channel(gpu, x, 8)
     oq, os_ = orc.quantize_per_channel(x, 8)
     assert bits_equal(q, oq.reshape(-1)) and bits_equal(s, os_)
+
+
+def test_per_channel_empty_slices(gpu, orc):
+    """channel_size 0: no element is read; min/max keep their FLT_MAX /
+    -FLT_MAX starting values, so every scale is FLT_MAX/127."""
+    say("per-channel, 5 empty slices")
+    dx, dq, ds = empty(4, np.float32), empty(16, np.int8), empty(5, np.float32)
+    rpl_amd.check(gpu.rplhip_quantize_per_channel(dx.ptr, 5, 0, dq.ptr, ds.ptr, None))
+    s = down(ds, np.float32, (5,))
+    _, os_ = orc.quantize_per_channel(np.zeros((5, 0), np.float32), 5)
+    assert bits_equal(s, os_) and s[0] == np.float32(np.finfo(np.float32).max) / np.float32(127)
 
 
 def test_symmetric_8192_squared_vs_oracle(gpu, orc):
