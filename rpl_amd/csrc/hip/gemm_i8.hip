@@ -804,104 +804,119 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
 }
 
 // ------------------- big-tile GEMM with A copied two k-steps at a time
-
-// Same tile, MFMA, B path and epilogues as k_gemm_i8_nt_dma<EPI, 256, BKN>,
-// with A copied in k-step pairs: one copy instruction moves 8 rows x 128
-// bytes (8 whole cache lines; the per-k-step copy moves 16 rows x 64 bytes,
-// half of 16 lines, and fetches each line twice).  A pair of A tiles fills a
-// 32 KB region laid out in 1 KB row groups: group g holds rows 8g..8g+7, the
-// first 512 bytes k-step 2p, the next 512 bytes k-step 2p+1, each as 8 rows
-// x 64 bytes with chunk c at slot c ^ swz(row).  Lane l of a copy writes
-// bytes 16l..16l+15 of one group, so it fetches k-step l/32, row 8g +
-// (l%32)/4, chunk (l%4) ^ swz(row).  (Keying the swizzle on row % 8 alone
-// leaves rows 8 apart on the same banks: measured 4 extra cycles per read.)  Fragment reads then see the per-k-step layout
-// (64-byte rows, the same swizzle) at a parity offset of 0 or 512 bytes.
 //
-// LDS: two A pair regions (64 KB) and four B stages (64 KB).  Iteration j
-// requests A pair (j+2, j+3) at its start when j is even, and B tile j+3
-// after its barrier; at the barrier a wave has issued, after the copies of
-// tile j+1 it waits for, 4 B + 8 A copies (j even) or 4 B copies (j odd).
-// Requires K % 128 == 0 (plus the conditions of k_gemm_i8_nt_dma).
+// Same tile (256 x 256 x 64, 4 waves of 128 x 128 on v_mfma_i32_32x32x32_i8),
+// B path and fused epilogues as k_gemm_i8_nt_dma<EPI, 256, BKN>, with A
+// copied in k-step pairs: one copy instruction moves 8 rows x 128 bytes (8
+// whole cache lines; the per-k-step copy moves 16 rows x 64 bytes, half of
+// 16 lines, and fetches each line twice).  A pair of A tiles fills a 32 KB
+// region laid out in 1 KB row groups: group g holds rows 8g..8g+7, the first
+// 512 bytes k-step 2p, the next 512 bytes k-step 2p+1, each as 8 rows x 64
+// bytes with chunk c at slot c ^ swz(row).  Lane l of a copy writes bytes
+// 16l..16l+15 of one group, so it fetches k-step l/32, row 8g + (l%32)/4,
+// chunk (l%4) ^ swz(row).  (Keying the swizzle on row % 8 alone leaves rows
+// 8 apart on the same banks: measured 4 extra cycles per read.)  Fragment
+// reads then see the per-k-step layout (64-byte rows, the same swizzle) at
+// a parity offset of 0 or 512 bytes.  LDS: two A pair slots (64 KB) and
+// four B stages (64 KB).
+//
+// Instruction schedule.  Each 32-k half issues its 16 MFMAs with exactly one
+// other memory instruction after each: the 12 (BKN; 8 for B [N,K]) fragment
+// reads of the next half, then 4 copies.  Copies issued in clusters stall
+// the wave in front of its next MFMA: with the copies bunched, a 64-k step
+// took 1262 cycles against 1024 of MFMA work, spread out 1082 (s_memtime
+// stamps per wave on MI355X, 8192^3).  Iteration j (tile j):
+//   first half:  MFMAs on k-half 0, reads of k-half 1, copies of B tile j+3
+//                into stage (j+3)%4 (tile j-1's, free since the barrier of
+//                iteration j-1);
+//   wait for tile j+1 (vmcnt(4) when j is odd, vmcnt(12) when even), barrier;
+//   second half: MFMAs on k-half 1, reads of tile j+1's k-half 0, and half
+//                an A pair: j odd, copies 0..3 of pair (j+3)/2 into tile j's
+//                pair slot (free since this barrier); j even, copies 4..7 of
+//                pair (j+2)/2.
+// Every iteration issues the same copies: copies of tiles past the end
+// re-load the last tile (or pair) into a stage or slot that no later read
+// uses, so the wait counts hold to the end and every access stays inside
+// the operands.  Requires K % 128 == 0 and the conditions of
+// k_gemm_i8_nt_dma.
+//
+// SPLIT (stream-K): the grid has one block per CU and block v (in an order
+// that gives each XCD a contiguous range) runs k-steps [v*L, (v+1)*L) of the
+// tiles' concatenated k-steps (tile t owns [t*nkt, (t+1)*nkt)), highest tile
+// first.  A tile whose k-steps span several blocks is finished by the block
+// holding its last k-step (the owner, which reaches it last); the others
+// (producers, which reach it first) store their int32 partial sums with
+// agent-coherent stores (sc1, what agent-scope atomics use; no L2 writeback
+// or invalidate), wait for them, and set their flag to this launch's epoch.
+// The owner polls each producer's flag (bounded: past kSplitSpinCycles it
+// computes that producer's k-steps itself, so the kernel finishes whatever
+// the scheduling), adds the partials (int32 sums are exact in any order)
+// and runs the epilogue.  Producers never wait, and owners wait only for
+// blocks earlier in the same range order.
 namespace dma {
 constexpr int kPairBytes = BM * 2 * BK;  // 256 rows x 128 k-bytes
 constexpr int kPairLoads = 8;            // 1 KB copies per wave per A pair
 }  // namespace dma
 
-template <int EPI, bool BKN>
-__global__ void __launch_bounds__(256, 1) k_gemm_i8_dma_pairs(const int8_t* __restrict__ A, uint32_t lda,
-                                                              const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
-                                                              uint32_t N, uint32_t K, EpiParams p) {
+struct SplitArgs {
+    uint32_t per_block;  // L: k-steps per block (even)
+    uint32_t epoch;      // flag value of this launch (never 0)
+    uint32_t* flags;     // [grid]
+    int32_t* partials;   // [grid][4 waves][64 KiB]
+};
+constexpr uint64_t kSplitSpinCycles = uint64_t(1) << 24;
+constexpr uint32_t kPartialWaveInts = 16384;  // 128 x 128 int32 per wave
+
+// Fragments of one 32-k half: A blocks and either B blocks (B [N,K]) or the
+// two 8-byte transposed halves of each B block (BKN).
+template <bool BKN>
+struct PairFrags;
+template <>
+struct PairFrags<false> {
+    v4i a[4], b[4];
+    __device__ v4i bv(int j) const { return b[j]; }
+};
+template <>
+struct PairFrags<true> {
+    v4i a[4];
+    v2i bl[4], bh[4];
+    __device__ v4i bv(int j) const { return (v4i){bl[j].x, bl[j].y, bh[j].x, bh[j].y}; }
+};
+
+// Tile index (already in XCD-contiguous order) -> tile row / column: groups
+// of kGroupM tile rows walked column by column (as rplhip::tile_of).
+__device__ __forceinline__ void tile_rc(uint32_t t, uint32_t tm, uint32_t tn, uint32_t& im, uint32_t& in) {
+    const uint32_t group = rplhip::kGroupM * tn;
+    const uint32_t g = t / group, first = g * rplhip::kGroupM;
+    const uint32_t gm = tm - first < rplhip::kGroupM ? tm - first : rplhip::kGroupM;
+    const uint32_t w = t - g * group;
+    im = first + w % gm;
+    in = w / gm;
+}
+
+template <int EPI, bool BKN, bool SPLIT>
+__global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restrict__ A, uint32_t lda,
+                                                          const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
+                                                          uint32_t N, uint32_t K, EpiParams p, SplitArgs sa) {
     using dma::BK;
     using dma::BM;
     using dma::kPairBytes;
-    using dma::kPairLoads;
-    constexpr int BN = 256, S = 4;
-    using G = dma::Geo<BN>;
-    constexpr int FN = G::FN, kLoadsB = G::kLoadsB;
+    constexpr int BN = 256, S = 4, FN = 4, kLoadsB = 4;
     constexpr int kBStage = BN * BK, kBBase = 2 * kPairBytes;
+    constexpr int kReads = BKN ? 12 : 8;  // fragment reads per half
     __shared__ __attribute__((aligned(1024))) int8_t smem[kBBase + S * kBStage];
+    __shared__ uint32_t s_ready;  // SPLIT: a producer's flag as the owner's wave 0 saw it
 
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t wm = wave / 2, wn = wave % 2;
-    uint32_t im, in;
-    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, im, in);
-    const uint32_t m0 = im * BM, n0 = in * BN;
-    const uint32_t rows_a = M - m0 < (uint32_t)BM ? M - m0 : BM;
-    const uint32_t rows_b = N - n0 < (uint32_t)BN ? N - n0 : BN;
-    const __amdgpu_buffer_rsrc_t rsrc_a = uniform_rsrc(A + (uint64_t)m0 * lda, rows_a * lda);
-    const __amdgpu_buffer_rsrc_t rsrc_b = BKN ? uniform_rsrc(B + n0, (K - 1) * ldb + rows_b)
-                                              : uniform_rsrc(B + (uint64_t)n0 * ldb, rows_b * ldb);
-
-    // A pair copies: wave w fills row groups 8w .. 8w+7 (rows 64w .. 64w+63);
-    // copy i covers rows R = 64w + 8i + a_rr.  The chunk swizzle is swz(R),
-    // with R % 32 = 8(i%4) + a_rr, so swz(R) = swz(a_rr) ^ 2(i%2): the
-    // column offset of copy i is a_col ^ 32(i%2).  Rows past M are clamped
-    // to the last row (never stored).
-    const uint32_t a_rr = (lane % 32) / 4;
-    const uint32_t a_row = wave * 64 + a_rr;
-    const uint32_t a_col = (lane / 32) * BK + ((lane % 4) ^ swz(a_rr)) * 16;
-    auto issue_a_pair = [&](uint32_t pair, int slot) {
-        int8_t* st = smem + slot * kPairBytes + wave * 8 * 1024;
-#pragma unroll
-        for (int i = 0; i < kPairLoads; i++) {
-            const uint32_t r = a_row + 8 * i;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr)(st + i * 1024), 16,
-                                                     (r < rows_a ? r : rows_a - 1) * lda + (a_col ^ (32 * (i % 2))),
-                                                     pair * 2 * BK, 0, 0);
-        }
-    };
-    // B copies as in k_gemm_i8_nt_dma.
-    uint32_t voff_b[4];
-#pragma unroll
-    for (int i = 0; i < kLoadsB; i++) {
-        if constexpr (BKN) {
-            if (i >= 2) continue;
-            const uint32_t r = wave * 16 + i * 4 + lane / 16;
-            const uint32_t c = (lane % 16) ^ dma::kn_swz(r % 8);
-            voff_b[i] = r * ldb + (16 * c < rows_b ? c : rows_b / 16 - 1) * 16;
-        } else {
-            const uint32_t r = wave * (BN / 4) + i * 16 + lane / 4;
-            voff_b[i] = (r < rows_b ? r : rows_b - 1) * ldb + ((lane % 4) ^ swz(r)) * 16;
-        }
-    }
-    auto issue_b = [&](uint32_t kt, uint32_t stage) {
-        int8_t* st = smem + kBBase + stage * kBStage;
-#pragma unroll
-        for (int i = 0; i < kLoadsB; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr)(st + (wave * (BN / 4) + i * 16) * BK), 16,
-                                                     voff_b[BKN ? i % 2 : i],
-                                                     BKN ? (kt * BK + 8 * (i / 2)) * ldb : kt * BK, 0, 0);
-    };
-
-    // Fragment reads.  A: row R = 128wm + 32i + fr lives in group R/8 at
-    // row R%8 = fr%8.  B: as in k_gemm_i8_nt_dma.
+    const uint32_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN, nkt = K / BK;
     const uint32_t fr = lane % 32;
     uint32_t foff_a[2], foff_b[2], boff[4];
 #pragma unroll
     for (int kk = 0; kk < 2; kk++) {
         foff_a[kk] = wm * 16 * 1024 + (fr / 8) * 1024 + (fr % 8) * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
-        if constexpr (!BKN) foff_b[kk] = wn * (BN / 2) * BK + fr * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
+        foff_b[kk] = wn * (BN / 2) * BK + fr * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
     }
     if constexpr (BKN) {
         const uint32_t g = lane / 16, e = (lane % 16) / 2, h = lane % 2;
@@ -909,115 +924,241 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_dma_pairs(const int8_t* __re
         for (int j = 0; j < 4; j++)
             boff[j] = (16 * (g / 2) + e) * 256 + ((8 * wn + 2 * j + g % 2) ^ dma::kn_swz(e)) * 16 + 8 * h;
     }
-    using F = dma::Frags<FN>;
+    using F = PairFrags<BKN>;
     using dma::lds_v2i;
-    // Tile j: A in pair slot (j/2)%2 at parity j%2, B in stage j%4.
-    auto fload = [&](uint32_t aslot, uint32_t par, uint32_t stage, int kk, F& f) {
-        const int8_t* sa = smem + aslot * kPairBytes + par * 512 + foff_a[kk];
-#pragma unroll
-        for (int i = 0; i < 4; i++) f.a[i] = *reinterpret_cast<const v4i*>(sa + i * 4096);
-        if constexpr (BKN) {
-            const int8_t* sb = smem + kBBase + stage * kBStage + kk * 32 * 256;
-#pragma unroll
-            for (int j = 0; j < FN; j++) {
-                const int8_t* pb = sb + boff[j];
-                const v2i lo = dma::tr8((lds_v2i)pb);
-                const v2i hi = dma::tr8((lds_v2i)(pb + 8 * 256));
-                f.b[j] = (v4i){lo.x, lo.y, hi.x, hi.y};
-            }
-        } else {
-            const int8_t* sb = smem + kBBase + stage * kBStage + foff_b[kk];
-#pragma unroll
-            for (int j = 0; j < FN; j++) f.b[j] = *reinterpret_cast<const v4i*>(sb + j * 32 * BK);
-        }
-    };
     v16i acc[4][4];
+
+    // k-steps [k0, k0 + nks) (even, >= 2) of the tile at (m0, n0), added
+    // into acc.  Leaves no copy in flight and every wave past a barrier.
+    auto mainloop = [&](uint32_t m0, uint32_t n0, uint32_t k0, uint32_t nks) {
+        const uint32_t rows_a = M - m0 < (uint32_t)BM ? M - m0 : BM;
+        const uint32_t rows_b = N - n0 < (uint32_t)BN ? N - n0 : BN;
+        const __amdgpu_buffer_rsrc_t rsrc_a = uniform_rsrc(A + (uint64_t)m0 * lda, rows_a * lda);
+        const __amdgpu_buffer_rsrc_t rsrc_b = BKN ? uniform_rsrc(B + n0, (K - 1) * ldb + rows_b)
+                                                  : uniform_rsrc(B + (uint64_t)n0 * ldb, rows_b * ldb);
+        // A pair copies: wave w fills row groups 8w .. 8w+7 (rows 64w ..
+        // 64w+63); copy i covers rows R = 64w + 8i + a_rr.  The chunk swizzle
+        // is swz(R), with R % 32 = 8(i%4) + a_rr, so swz(R) = swz(a_rr) ^
+        // 2(i%2): the column offset of copy i is a_col ^ 32(i%2).  Rows past M
+        // are clamped to the last row (never stored).
+        const uint32_t a_rr = (lane % 32) / 4;
+        const uint32_t a_row = wave * 64 + a_rr;
+        const uint32_t a_col = (lane / 32) * BK + ((lane % 4) ^ swz(a_rr)) * 16;
+        auto copy_a = [&](uint32_t pair, int slot, int i) {
+            int8_t* st = smem + slot * kPairBytes + wave * 8 * 1024;
+            const uint32_t r = a_row + 8 * i;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr)(st + i * 1024), 16,
+                                                     (r < rows_a ? r : rows_a - 1) * lda + (a_col ^ (32 * (i % 2))),
+                                                     (k0 + 2 * pair) * BK, 0, 0);
+        };
+        // B copies as in k_gemm_i8_nt_dma.
+        uint32_t voff_b[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+        for (int i = 0; i < kLoadsB; i++) {
+            if constexpr (BKN) {
+                if (i >= 2) continue;
+                const uint32_t r = wave * 16 + i * 4 + lane / 16;
+                const uint32_t c = (lane % 16) ^ dma::kn_swz(r % 8);
+                voff_b[i] = r * ldb + (16 * c < rows_b ? c : rows_b / 16 - 1) * 16;
+            } else {
+                const uint32_t r = wave * (BN / 4) + i * 16 + lane / 4;
+                voff_b[i] = (r < rows_b ? r : rows_b - 1) * ldb + ((lane % 4) ^ swz(r)) * 16;
+            }
+        }
+        auto copy_b = [&](uint32_t kt, uint32_t stage, int i) {
+            int8_t* st = smem + kBBase + stage * kBStage;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr)(st + (wave * (BN / 4) + i * 16) * BK), 16,
+                                                     voff_b[BKN ? i % 2 : i],
+                                                     BKN ? ((k0 + kt) * BK + 8 * (i / 2)) * ldb : (k0 + kt) * BK, 0, 0);
+        };
+        // Read r of tile (aslot, par, stage), k-half kk: r < 4 is A block r;
+        // then B block (r-4) (B [N,K]) or the low / high transposed half of B
+        // block (r-4)/2 (BKN).
+        auto read_one = [&](uint32_t aslot, uint32_t par, uint32_t stage, int kk, int r, F& f) {
+            if (r < 4) {
+                const int8_t* sa_ = smem + aslot * kPairBytes + par * 512 + foff_a[kk];
+                f.a[r] = *reinterpret_cast<const v4i*>(sa_ + r * 4096);
+            } else if constexpr (BKN) {
+                const int j = (r - 4) / 2, hi = (r - 4) % 2;
+                const int8_t* pb = smem + kBBase + stage * kBStage + kk * 32 * 256 + boff[j] + hi * 8 * 256;
+                const v2i t = dma::tr8((lds_v2i)pb);
+                if (hi)
+                    f.bh[j] = t;
+                else
+                    f.bl[j] = t;
+            } else {
+                f.b[r - 4] = *reinterpret_cast<const v4i*>(smem + kBBase + stage * kBStage + foff_b[kk] +
+                                                            (r - 4) * 32 * BK);
+            }
+        };
+        // Order of the next half's reads: A block 0, the B blocks, A blocks
+        // 1..3 -- the order in which its MFMAs first use them.
+        auto read_at = [](int m) {
+            if constexpr (BKN) {
+                constexpr int o[12] = {0, 4, 5, 6, 7, 8, 9, 10, 11, 1, 2, 3};
+                return o[m];
+            } else {
+                constexpr int o[8] = {0, 4, 5, 6, 7, 1, 2, 3};
+                return o[m];
+            }
+        };
+        // One half: MFMA m on `cur`, then read m of `nxt` (m < kReads) or
+        // copy m - kReads (the half's 4 copies).
+        auto half = [&](const F& cur, F& nxt, uint32_t aslot, uint32_t par, uint32_t stage, int kk, auto copy) {
+            static_for<16>([&](auto Mc) {
+                constexpr int m = decltype(Mc)::value;
+                acc[m / 4][m % 4] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[m / 4], cur.bv(m % 4),
+                                                                         acc[m / 4][m % 4], 0, 0, 0);
+                if constexpr (m < kReads)
+                    read_one(aslot, par, stage, kk, read_at(m), nxt);
+                else if constexpr (m < kReads + 4)
+                    copy(m - kReads);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        };
+
+        // Prologue: A pair 0 (tiles 0, 1), B tiles 0..2, copies 0..3 of A
+        // pair 1; tile 0 landed.
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] = (v16i){};
-    auto mma = [&](const F& f) {
+        for (int i = 0; i < 8; i++) copy_a(0, 0, i);
+#pragma unroll
+        for (int t = 0; t < 3; t++) {
+            const uint32_t src = (uint32_t)t < nks ? t : nks - 1;
+#pragma unroll
+            for (int i = 0; i < 4; i++) copy_b(src, t, i);
+        }
+        const uint32_t npairs = nks / 2;
+#pragma unroll
+        for (int i = 0; i < 4; i++) copy_a(npairs > 1 ? 1 : 0, 1, i);
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(12, 0));
+        __builtin_amdgcn_s_barrier();
+        F f0, f1;
+        static_for<kReads>([&](auto R) { read_one(0, 0, 0, 0, decltype(R)::value, f0); });
+
+        auto iter = [&](auto U, uint32_t kt) {
+            constexpr int u = decltype(U)::value;  // kt % 4 == 0
+            const uint32_t j = kt + u;
+            __builtin_amdgcn_sched_barrier(0);
+            const uint32_t tb = j + 3 < nks ? j + 3 : nks - 1;
+            half(f0, f1, (u / 2) % 2, u % 2, u, 1, [&](int c) { copy_b(tb, (u + 3) % S, c); });
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(u % 2 == 1 ? 4 : 12, 0));
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (u % 2 == 1) {
+                const uint32_t pa = (j + 3) / 2 < npairs ? (j + 3) / 2 : npairs - 1;
+                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, (u + 1) % S, 0,
+                     [&](int c) { copy_a(pa, (u / 2) % 2, c); });
+            } else {
+                const uint32_t pa = (j + 2) / 2 < npairs ? (j + 2) / 2 : npairs - 1;
+                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, (u + 1) % S, 0,
+                     [&](int c) { copy_a(pa, ((u + 2) / 2) % 2, 4 + c); });
+            }
+        };
+        uint32_t kt = 0;
+        for (; kt + S <= nks; kt += S) static_for<S>([&](auto U) { iter(U, kt); });
+        if (kt < nks) static_for<2>([&](auto U) { iter(U, kt); });  // nks % 4 == 2
+        // The trailing copies land before the LDS is reused or released.
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+        __builtin_amdgcn_s_barrier();
+    };
+    auto zero_acc = [&] {
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int j = 0; j < FN; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < FN; j++) acc[i][j] = (v16i){};
     };
-    // One half's order: a fragment read after each early MFMA, then the
-    // half's copies spread over the remaining MFMAs.
-    auto pin = [&](auto copies_c) {
-        constexpr int copies = decltype(copies_c)::value;
-        constexpr int reads = 4 + (BKN ? 2 : 1) * FN, rest = 4 * FN - reads;
-        static_for<reads>([&](auto) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-        });
-        if constexpr (copies > 0) {
-            static_for<rest>([&](auto) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x020, (copies + rest - 1) / rest, 0);
-            });
-        }
-    };
-
-    const uint32_t nk = K / BK;  // even, >= 2
-    // Prologue: A pair 0, B tiles 0 .. 2; tile 0 landed (B 1, 2 may not).
-    issue_a_pair(0, 0);
-    issue_b(0, 0);
-    issue_b(1, 1);
-    if (nk > 2) {
-        issue_b(2, 2);
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kLoadsB, 0));
-    } else {
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLoadsB, 0));
-    }
-    __builtin_amdgcn_s_barrier();
-    F f0, f1;
-    fload(0, 0, 0, 0, f0);
-
-    uint32_t kt = 0;
-    for (; kt + 2 * S - 1 <= nk; kt += S) {
-        static_for<S>([&](auto U) {
-            constexpr int u = decltype(U)::value;  // kt % 4 == 0: tile kt+u has slot (u/2)%2, parity u%2
-            __builtin_amdgcn_sched_barrier(0);
-            if constexpr (u % 2 == 0) issue_a_pair((kt + u) / 2 + 1, ((u + 2) / 2) % 2);
-            fload((u / 2) % 2, u % 2, u, 1, f1);
-            mma(f0);
-            pin(std::integral_constant<int, u % 2 == 0 ? kPairLoads : 0>{});
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_waitcnt(waitcnt_imm(u % 2 == 0 ? kLoadsB + kPairLoads : kLoadsB, 0));
-            __builtin_amdgcn_s_barrier();
-            __builtin_amdgcn_sched_barrier(0);
-            issue_b(kt + u + 3, (u + 3) % S);
-            fload(((u + 1) / 2) % 2, (u + 1) % 2, (u + 1) % S, 0, f0);
-            mma(f1);
-            pin(std::integral_constant<int, kLoadsB>{});
-            __builtin_amdgcn_sched_barrier(0);
-        });
-    }
-    // Last iterations: requests only while tiles remain.
-    for (; kt < nk; kt++) {
-        const bool more = kt + 2 < nk;
-        if (kt % 2 == 0 && more) issue_a_pair(kt / 2 + 1, (kt / 2 + 1) % 2);
-        fload((kt / 2) % 2, kt % 2, kt % S, 1, f1);
-        mma(f0);
-        if (!more)
-            __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
-        else if (kt % 2 == 0)
-            __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLoadsB + kPairLoads, 0));
+    auto epilogue = [&](uint32_t m0, uint32_t n0) {
+        if (m0 + BM <= M && n0 + BN <= N && p.ldc <= kFullEpiMaxLdc)
+            epilogue_tile_full<EPI, 4, FN, 4>(p, acc, m0 + wm * 128, n0 + wn * (BN / 2), lane);
         else
-            __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLoadsB, 0));
-        __builtin_amdgcn_s_barrier();
-        if (kt + 3 < nk) issue_b(kt + 3, (kt + 3) % S);
-        if (kt + 1 < nk) fload(((kt + 1) / 2) % 2, (kt + 1) % 2, (kt + 1) % S, 0, f0);
-        mma(f1);
-    }
+            epilogue_tile<EPI, 4, FN, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * (BN / 2) + lane % 32,
+                                         M, N);
+    };
 
-    if (m0 + BM <= M && n0 + BN <= N && p.ldc <= kFullEpiMaxLdc)
-        epilogue_tile_full<EPI, 4, FN, 4>(p, acc, m0 + wm * 128, n0 + wn * (BN / 2), lane);
-    else
-        epilogue_tile<EPI, 4, FN, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * (BN / 2) + lane % 32, M,
-                                     N);
+    if constexpr (!SPLIT) {
+        uint32_t im, in;
+        tile_of(blockIdx.x, tm, tn, im, in);
+        zero_acc();
+        mainloop(im * BM, in * BN, 0, nkt);
+        epilogue(im * BM, in * BN);
+    } else {
+        // Range order: the XCDs (block b runs on XCD b % 8) take contiguous
+        // ranges of blocks, so neighbouring tiles share an XCD's L2.
+        const uint32_t G = gridDim.x, x = blockIdx.x % rplhip::kXcds, q = G / rplhip::kXcds,
+                       r = G % rplhip::kXcds;
+        const uint32_t v = x * q + (x < r ? x : r) + blockIdx.x / rplhip::kXcds;
+        const uint64_t L = sa.per_block, total = (uint64_t)tm * tn * nkt;
+        const uint64_t s0 = (uint64_t)v * L;
+        uint64_t e = s0 + L < total ? s0 + L : total;
+        // A block's partial (at most one: the first segment it runs) lives
+        // in slot v: 4 waves x 64 KiB, lane-interleaved 16-byte pieces.
+        auto slot_rsrc = [&](uint32_t blk) {
+            return uniform_rsrc(sa.partials + ((uint64_t)blk * 4 + wave) * kPartialWaveInts, kPartialWaveInts * 4);
+        };
+        while (e > s0) {
+            const uint32_t t = (uint32_t)((e - 1) / nkt);
+            const uint64_t ts = (uint64_t)t * nkt;
+            const uint64_t sb = s0 > ts ? s0 : ts;
+            const uint32_t k0 = (uint32_t)(sb - ts), k1 = (uint32_t)(e - ts);
+            uint32_t im, in;
+            tile_rc(t, tm, tn, im, in);
+            zero_acc();
+            mainloop(im * BM, in * BN, k0, k1 - k0);
+            if (k0 == 0 && k1 == nkt) {
+                epilogue(im * BM, in * BN);
+            } else if (k1 < nkt) {
+                // Producer: publish the partial sums, then the flag.
+                const __amdgpu_buffer_rsrc_t rs = slot_rsrc(v);
+                static_for<64>([&](auto I) {
+                    constexpr int idx = decltype(I)::value;
+                    constexpr int i = idx / 16, j = (idx / 4) % 4, r4 = idx % 4;
+                    const v4i w = (v4i){acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2],
+                                        acc[i][j][4 * r4 + 3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(w, rs, lane * 16, idx * 1024, 16 /* sc1 */);
+                });
+                __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+                __builtin_amdgcn_s_barrier();
+                if (threadIdx.x == 0) __hip_atomic_store(sa.flags + v, sa.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                // Owner: the producers are the blocks from ts / L to v - 1.
+                const uint32_t first = (uint32_t)(ts / L);
+                for (uint32_t pb = first; pb < v; pb++) {
+                    if (threadIdx.x == 0) {
+                        const uint64_t t_start = __builtin_amdgcn_s_memtime();
+                        uint32_t ok = 0;
+                        while (!(ok = __hip_atomic_load(sa.flags + pb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                                      sa.epoch) &&
+                               __builtin_amdgcn_s_memtime() - t_start < kSplitSpinCycles)
+                            __builtin_amdgcn_s_sleep(2);
+                        s_ready = ok;
+                    }
+                    __syncthreads();
+                    const uint32_t ready = __builtin_amdgcn_readfirstlane(s_ready);
+                    __syncthreads();
+                    if (ready) {
+                        const __amdgpu_buffer_rsrc_t rs = slot_rsrc(pb);
+                        static_for<64>([&](auto I) {
+                            constexpr int idx = decltype(I)::value;
+                            constexpr int i = idx / 16, j = (idx / 4) % 4, r4 = idx % 4;
+                            const v4i w = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, idx * 1024, 16 /* sc1 */);
+                            acc[i][j][4 * r4] = wrap_add(acc[i][j][4 * r4], w.x);
+                            acc[i][j][4 * r4 + 1] = wrap_add(acc[i][j][4 * r4 + 1], w.y);
+                            acc[i][j][4 * r4 + 2] = wrap_add(acc[i][j][4 * r4 + 2], w.z);
+                            acc[i][j][4 * r4 + 3] = wrap_add(acc[i][j][4 * r4 + 3], w.w);
+                        });
+                    } else {
+                        // Not published in time: compute producer pb's
+                        // k-steps of this tile here instead.
+                        const uint64_t ps = (uint64_t)pb * L > ts ? (uint64_t)pb * L : ts;
+                        const uint64_t pe = ((uint64_t)pb + 1) * L < ts + nkt ? ((uint64_t)pb + 1) * L : ts + nkt;
+                        mainloop(im * BM, in * BN, (uint32_t)(ps - ts), (uint32_t)(pe - ps));
+                    }
+                }
+                epilogue(im * BM, in * BN);
+            }
+            e = sb;
+        }
+    }
 }
 
 // --------------------------------------------------- skinny (M <= 16) GEMM
@@ -1477,7 +1618,7 @@ bool use_dma() {
     return !(env && env[0] == '0');
 }
 
-// A copied in k-step pairs (k_gemm_i8_dma_pairs) when K % 128 == 0, unless
+// A copied in k-step pairs (k_gemm_i8_pairs) when K % 128 == 0, unless
 // RPLHIP_I8_PAIRS=0 (for A/B timing only).
 bool use_pairs(uint32_t K) {
     static const char* env = getenv("RPLHIP_I8_PAIRS");
@@ -1620,8 +1761,8 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
             const EpiParams p2 = shift_cols(p, n1);
             const uint32_t tiles1 = (uint32_t)(mt * (n1 / 256)), tiles2 = (uint32_t)(mt * ((N - n1 + 127) / 128));
             if (use_pairs(K))
-                hipLaunchKernelGGL((k_gemm_i8_dma_pairs<EPI, false>), dim3(tiles1), dim3(dma::kThreads), 0, s, A, lda,
-                                   B, ldb, M, n1, K, p);
+                hipLaunchKernelGGL((k_gemm_i8_pairs<EPI, false, false>), dim3(tiles1), dim3(dma::kThreads), 0, s, A, lda,
+                                   B, ldb, M, n1, K, p, SplitArgs{});
             else
                 hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256>), dim3(tiles1), dim3(dma::kThreads), 0, s, A, lda, B,
                                    ldb, M, n1, K, p);
@@ -1632,8 +1773,8 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
         if (dma_ok) {
             const uint64_t tiles = mt * ((N + 255) / 256);
             if (use_pairs(K))
-                hipLaunchKernelGGL((k_gemm_i8_dma_pairs<EPI, false>), dim3((uint32_t)tiles), dim3(dma::kThreads), 0,
-                                   s, A, lda, B, ldb, M, N, K, p);
+                hipLaunchKernelGGL((k_gemm_i8_pairs<EPI, false, false>), dim3((uint32_t)tiles), dim3(dma::kThreads),
+                                   0, s, A, lda, B, ldb, M, N, K, p, SplitArgs{});
             else
                 hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256>), dim3((uint32_t)tiles), dim3(dma::kThreads), 0, s, A,
                                    lda, B, ldb, M, N, K, p);
@@ -1671,8 +1812,8 @@ int launch_kn(const int8_t* A, const int8_t* B, uint32_t M, uint32_t N, uint32_t
               hipStream_t s) {
     const uint32_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
     if (use_pairs(K))
-        hipLaunchKernelGGL((k_gemm_i8_dma_pairs<EPI, true>), dim3(tiles), dim3(dma::kThreads), 0, s, A, K, B, N, M,
-                           N, K, p);
+        hipLaunchKernelGGL((k_gemm_i8_pairs<EPI, true, false>), dim3(tiles), dim3(dma::kThreads), 0, s, A, K, B, N,
+                           M, N, K, p, SplitArgs{});
     else
         hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256, true>), dim3(tiles), dim3(dma::kThreads), 0, s, A, K, B, N, M,
                            N, K, p);

@@ -258,8 +258,9 @@ def _requant_f32(acc, sa, sb, sc):
 # it first otherwise (5900, 3000).  (1800, 3000, 448) has too few 256 x 256
 # tiles and takes 256 x 128 ones (192 of them), with ragged M and N edges.
 # K % 128 == 0 (896, 256, 128) copies A two k-steps at a time
-# (k_gemm_i8_dma_pairs): K = 896 runs its steady loop and a 6-tile tail,
-# K = 256 and 128 only the tail (4 and 2 tiles).
+# (k_gemm_i8_pairs): K = 896 runs three 4-k-step rounds of its loop and the
+# 2-k-step remainder (with the copies past the end re-loading the last
+# tile), K = 256 one round, K = 128 only the remainder.
 # (4096, 3072, 128) is one k-step pair on the pairs kernel, (4096, 4096, 64)
 # a single k-step on the per-k-step kernel.
 # K % 16 == 0 but K % 64 != 0 with at least two 256 x 256 tiles per CU
