@@ -263,6 +263,9 @@ def _requant_f32(acc, sa, sb, sc):
 # tile), K = 256 one round, K = 128 only the remainder.
 # (4096, 3072, 128) is one k-step pair on the pairs kernel, (4096, 4096, 64)
 # a single k-step on the per-k-step kernel.
+# (3830, 5104 | 5110, 1024): 300 big tiles (two rounds, the second mostly
+# idle) on the pairs kernel, 16 k-steps each, ragged M and N (5104: B [K,N]
+# read in place by gemm_int8; 5110: through the transposed copy).
 # K % 16 == 0 but K % 64 != 0 with at least two 256 x 256 tiles per CU
 # (6144 x 6144: 576 tiles, 4096 x 8192: 512) takes the register-staged
 # 256 x 256 kernel (k_gemm_i8_nt<CfgBig>): K = 848 is 13 whole 64-k tiles and
@@ -270,7 +273,7 @@ def _requant_f32(acc, sa, sb, sc):
 # same; gemm_int8 reaches it through the transposed copy of B.
 BIG = [(5890, 5900, 832), (5890, 5888, 832), (6144, 6144, 448), (1800, 3000, 448), (2900, 4400, 448),
        (5890, 5888, 896), (5890, 5900, 896), (2900, 4400, 256), (4096, 3072, 128), (4096, 4096, 64),
-       (6144, 6144, 848), (4096, 8192, 592)]
+       (6144, 6144, 848), (4096, 8192, 592), (3830, 5104, 1024), (3830, 5110, 1024)]
 
 
 @pytest.mark.parametrize("M,N,K", BIG)
