@@ -73,10 +73,15 @@ __global__ void __launch_bounds__(kThreads) k_fill(float* __restrict__ x, uint64
 constexpr int kColTile = 64;
 constexpr int kRowLanes = kThreads / kColTile;
 
+// DX: also pass the gradient through to backward_add's other operand,
+// dx = dx + dy (overwrite: 0.0f + dy), as k_accumulate does; every element
+// of dy is visited exactly once.
+template <bool DX>
 __global__ void __launch_bounds__(kThreads) k_colsum_partial(const float* __restrict__ dy, uint64_t n,
                                                              uint64_t rows, uint64_t nb,
                                                              uint64_t rows_per_split,
-                                                             float* __restrict__ part) {
+                                                             float* __restrict__ part, float* __restrict__ dx,
+                                                             int dx_overwrite) {
     __shared__ float red[kRowLanes][kColTile];
     uint64_t c = (uint64_t)blockIdx.x * kColTile + threadIdx.x % kColTile;
     int lane_r = threadIdx.x / kColTile;
@@ -99,9 +104,20 @@ __global__ void __launch_bounds__(kThreads) k_colsum_partial(const float* __rest
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 if (ok[j]) g += v[j];
+            if constexpr (DX) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint64_t i = (r + j * kRowLanes) * nb + c;
+                    if (ok[j]) dx[i] = (dx_overwrite ? 0.0f : dx[i]) + v[j];
+                }
+            }
         }
         for (; r < r1; r += kRowLanes)
-            if (r * nb + c < n) g += dy[r * nb + c];
+            if (r * nb + c < n) {
+                const float v = dy[r * nb + c];
+                g += v;
+                if constexpr (DX) dx[r * nb + c] = (dx_overwrite ? 0.0f : dx[r * nb + c]) + v;
+            }
     }
     red[lane_r][threadIdx.x % kColTile] = g;
     __syncthreads();
@@ -174,14 +190,41 @@ __global__ void __launch_bounds__(kThreads) k_sqerr_finish(const float* __restri
     if (threadIdx.x == 0) loss[0] = acc / (float)n;  // rpl_core.c:457
 }
 
+// n <= kSqerrSingleMax: the whole sum in one block (one launch instead of
+// partials plus a finishing block): a strided sum per thread, a 64-lane
+// butterfly, then the 16 wave sums in order.
+constexpr int kSqerrThreads = 1024;
+constexpr uint64_t kSqerrSingleMax = uint64_t(1) << 18;
+__global__ void __launch_bounds__(kSqerrThreads) k_sqerr_single(const float* __restrict__ p,
+                                                                const float* __restrict__ t, uint64_t n,
+                                                                float* __restrict__ loss) {
+    __shared__ float s[kSqerrThreads / 64];
+    float acc = 0;
+#pragma unroll 8
+    for (uint64_t i = threadIdx.x; i < n; i += kSqerrThreads) {
+        const float d = p[i] - t[i];
+        acc += d * d;
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (threadIdx.x % 64 == 0) s[threadIdx.x / 64] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float tot = 0;
+        for (int w = 0; w < kSqerrThreads / 64; w++) tot += s[w];
+        loss[0] = tot / (float)n;  // rpl_core.c:457
+    }
+}
+
 // rpl_core.c:441-444.  The update contracts to fma(g0 * factor, p - t, dp);
 // overwrite uses +0.0 for dp, as a zeroed gradient would hold.
+// g0p NULL: the root gradient's value is g0v (a gradient marked, not
+// written, by tensor_backward).
 __global__ void __launch_bounds__(kThreads) k_mse_backward(const float* __restrict__ p,
                                                            const float* __restrict__ t, uint64_t n,
-                                                           const float* __restrict__ g0p,
+                                                           const float* __restrict__ g0p, float g0v,
                                                            float* __restrict__ dp, int overwrite) {
     float factor = 2.0f / (float)n;
-    float g0 = *g0p;
+    float g0 = g0p ? *g0p : g0v;
     GRID_STRIDE(i, n) { dp[i] = (overwrite ? 0.0f : dp[i]) + g0 * factor * (p[i] - t[i]); }
 }
 
@@ -217,6 +260,40 @@ __global__ void __launch_bounds__(kThreads) k_act(const float* __restrict__ x, f
 //   v = fma(mom, v, (1 - damp) * g)     momentum buffer
 //   g = fma(mom, v, g)                  Nesterov (grad updated in place)
 //   p = fma(-lr, d, p)                  d = g (Nesterov / no momentum) or v
+// One element of optimizer_sgd_step (src/rpl_training.c:70-114).
+__device__ __forceinline__ void sgd_one(float* __restrict__ p, float* __restrict__ g, float* __restrict__ v,
+                                        uint64_t i, float lr, float mom, float keep, float wd, int nesterov) {
+#pragma clang fp contract(off)
+    const float pi = p[i];
+    float gi = g[i];
+    if (wd != 0.0f) gi = __fmaf_rn(wd, pi, gi);
+    float d = gi;
+    if (mom != 0.0f) {
+        const float vi = __fmaf_rn(mom, v[i], keep * gi);
+        v[i] = vi;
+        if (nesterov) {
+            gi = __fmaf_rn(mom, vi, gi);
+            d = gi;
+        } else {
+            d = vi;
+        }
+    }
+    g[i] = gi;
+    p[i] = __fmaf_rn(-lr, d, pi);
+}
+
+// Several parameter tensors in one launch: tensor k gets the blocks
+// [first[k], first[k+1]).
+__global__ void __launch_bounds__(kThreads) k_sgd_multi(RplSgdTensors ts, float lr, float mom, float damp, float wd,
+                                                        int nesterov) {
+    int k = 0;
+    while (k + 1 < ts.count && blockIdx.x >= ts.first[k + 1]) k++;
+    const uint32_t b = blockIdx.x - ts.first[k], nb = ts.first[k + 1] - ts.first[k];
+    const float keep = 1.0f - damp;
+    for (uint64_t i = (uint64_t)b * kThreads + threadIdx.x; i < ts.n[k]; i += (uint64_t)nb * kThreads)
+        sgd_one(ts.p[k], ts.g[k], ts.v[k], i, lr, mom, keep, wd, nesterov);
+}
+
 __global__ void __launch_bounds__(kThreads) k_sgd_step(float* __restrict__ p, float* __restrict__ g,
                                                        float* __restrict__ v, uint64_t n, float lr, float mom,
                                                        float damp, float wd, int nesterov) {
@@ -317,34 +394,88 @@ int rplhip_bias_grad(const float* dy, uint64_t n, float* db, uint64_t nb, rplhip
     return rplhip__bias_grad(dy, n, db, nb, 0, stream);
 }
 
+}  // extern "C"
+
+namespace {
+// Row splits of the bias-gradient reduction of dy [n / nb rows, nb].
+struct ColsumPlan {
+    uint64_t full_rows, cx, splits, rps;
+};
+ColsumPlan colsum_plan(uint64_t n, uint64_t nb) {
+    ColsumPlan c;
+    // backward_add's j-loop visits i, i+nb, ... < n: ceil(n/nb) rows.
+    c.full_rows = (n + nb - 1) / nb;
+    c.cx = (nb + kColTile - 1) / kColTile;
+    // Enough row splits to put ~4 blocks on every CU, each split >= 64 rows.
+    uint64_t want = (4ull * cu_count() + c.cx - 1) / c.cx;
+    uint64_t splits = c.full_rows / 64;
+    if (splits > want) splits = want;
+    if (splits < 1) splits = 1;
+    if (splits > 65535) splits = 65535;
+    c.rps = (c.full_rows + splits - 1) / splits;
+    splits = (c.full_rows + c.rps - 1) / c.rps;
+    c.splits = splits < 1 ? 1 : splits;
+    return c;
+}
+}  // namespace
+
+extern "C" {
+
 int rplhip__bias_grad(const float* dy, uint64_t n, float* db, uint64_t nb, int overwrite, rplhip_stream_t stream) {
     if (nb == 0) return RPLHIP_OK;
     NEED(dy && db, "rplhip_bias_grad");
     RPLHIP_REQUIRE_DEVICE();
     hipStream_t s = as_stream(stream);
-    // backward_add's j-loop visits i, i+nb, ... < n: ceil(n/nb) rows.
-    uint64_t full_rows = (n + nb - 1) / nb;
-    uint64_t cx = (nb + kColTile - 1) / kColTile;
-    // Enough row splits to put ~4 blocks on every CU, each split >= 64 rows.
-    uint64_t want = (4ull * cu_count() + cx - 1) / cx;
-    uint64_t splits = full_rows / 64;
-    if (splits > want) splits = want;
-    if (splits < 1) splits = 1;
-    if (splits > 65535) splits = 65535;
-    uint64_t rps = (full_rows + splits - 1) / splits;
-    splits = (full_rows + rps - 1) / rps;
-    if (splits < 1) splits = 1;
+    const ColsumPlan c = colsum_plan(n, nb);
     void* ws = nullptr;
-    int st = ws_alloc(&ws, sizeof(float) * splits * nb, s);
+    int st = ws_alloc(&ws, sizeof(float) * c.splits * nb, s);
     if (st) return st;
     // A ragged last row (n % nb != 0, columns < n % nb get one more term) is
     // handled by the r*nb + c < n bound in the partial kernel.
-    hipLaunchKernelGGL(k_colsum_partial, dim3((unsigned)cx, (unsigned)splits), dim3(kThreads), 0, s, dy, n,
-                       full_rows, nb, rps, (float*)ws);
-    hipLaunchKernelGGL(k_colsum_finish, dim3((unsigned)cx), dim3(kThreads), 0, s, (const float*)ws, (int)splits, nb,
-                       db, overwrite);
+    hipLaunchKernelGGL(k_colsum_partial<false>, dim3((unsigned)c.cx, (unsigned)c.splits), dim3(kThreads), 0, s, dy,
+                       n, c.full_rows, nb, c.rps, (float*)ws, (float*)nullptr, 0);
+    hipLaunchKernelGGL(k_colsum_finish, dim3((unsigned)c.cx), dim3(kThreads), 0, s, (const float*)ws, (int)c.splits,
+                       nb, db, overwrite);
     st = check_launch("bias_grad");
     ws_free(ws, s);
+    return st;
+}
+
+int rplhip__add_backward_begin(const float* dy, uint64_t n, float* dx, int dx_overwrite, uint64_t nb, RplColsum* cs,
+                               rplhip_stream_t stream) {
+    cs->ws = nullptr;
+    cs->splits = 0;
+    cs->nb = nb;
+    if (n == 0) return RPLHIP_OK;
+    NEED(dy && dx, "rplhip_add_backward");
+    if (nb == 0) return rplhip__accumulate(dy, dx, n, dx_overwrite, stream);
+    RPLHIP_REQUIRE_DEVICE();
+    hipStream_t s = as_stream(stream);
+    const ColsumPlan c = colsum_plan(n, nb);
+    int st = ws_alloc(&cs->ws, sizeof(float) * c.splits * nb, s);
+    if (st) return st;
+    cs->splits = c.splits;
+    hipLaunchKernelGGL(k_colsum_partial<true>, dim3((unsigned)c.cx, (unsigned)c.splits), dim3(kThreads), 0, s, dy,
+                       n, c.full_rows, nb, c.rps, (float*)cs->ws, dx, dx_overwrite);
+    st = check_launch("add_backward");
+    if (st) {
+        ws_free(cs->ws, s);
+        cs->ws = nullptr;
+    }
+    return st;
+}
+
+int rplhip__add_backward_finish(RplColsum* cs, float* db, int db_overwrite, rplhip_stream_t stream) {
+    if (!cs->ws) return RPLHIP_OK;
+    hipStream_t s = as_stream(stream);
+    int st = RPLHIP_OK;
+    if (db) {
+        hipLaunchKernelGGL(k_colsum_finish, dim3((unsigned)((cs->nb + kColTile - 1) / kColTile)), dim3(kThreads), 0,
+                           s, (const float*)cs->ws, (int)cs->splits, cs->nb, db, db_overwrite);
+        st = check_launch("add_backward (bias)");
+    }
+    ws_free(cs->ws, s);
+    cs->ws = nullptr;
     return st;
 }
 
@@ -353,6 +484,10 @@ int rplhip_mse_loss(const float* pred, const float* target, uint64_t n, float* l
     NEED(pred && target && loss, "rplhip_mse_loss");
     RPLHIP_REQUIRE_DEVICE();
     hipStream_t s = as_stream(stream);
+    if (n <= kSqerrSingleMax) {
+        hipLaunchKernelGGL(k_sqerr_single, dim3(1), dim3(kSqerrThreads), 0, s, pred, target, n, loss);
+        return check_launch("mse_loss");
+    }
     int g = grid_for(n);
     if (g > 1024) g = 1024;
     void* ws = nullptr;
@@ -365,19 +500,20 @@ int rplhip_mse_loss(const float* pred, const float* target, uint64_t n, float* l
     return st;
 }
 
-int rplhip__mse_backward(const float* pred, const float* target, uint64_t n, const float* g0, float* dpred,
-                         int overwrite, rplhip_stream_t stream) {
+int rplhip__mse_backward(const float* pred, const float* target, uint64_t n, const float* g0, float g0_value,
+                         float* dpred, int overwrite, rplhip_stream_t stream) {
     if (n == 0) return RPLHIP_OK;
-    NEED(pred && target && g0 && dpred, "rplhip_mse_backward");
+    NEED(pred && target && dpred, "rplhip_mse_backward");
     RPLHIP_REQUIRE_DEVICE();
     hipLaunchKernelGGL(k_mse_backward, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), pred,
-                       target, n, g0, dpred, overwrite);
+                       target, n, g0, g0_value, dpred, overwrite);
     return check_launch("mse_backward");
 }
 
 int rplhip_mse_backward(const float* pred, const float* target, uint64_t n, const float* g0,
                         float* dpred, rplhip_stream_t stream) {
-    return rplhip__mse_backward(pred, target, n, g0, dpred, 0, stream);
+    if (!g0) return fail(RPLHIP_ERR_INVALID, "rplhip_mse_backward: NULL pointer");
+    return rplhip__mse_backward(pred, target, n, g0, 0.0f, dpred, 0, stream);
 }
 
 static int launch_act(int act, const float* x, float* y, uint64_t n, rplhip_stream_t stream, const char* what) {
@@ -415,6 +551,23 @@ int rplhip_sgd_step(float* param, float* grad, float* velocity, uint64_t n, floa
     hipLaunchKernelGGL(k_sgd_step, dim3(grid_for(n)), dim3(kThreads), 0, as_stream(stream), param, grad, velocity, n,
                        lr, momentum, dampening, weight_decay, nesterov);
     return check_launch("sgd_step");
+}
+
+int rplhip__sgd_step_multi(RplSgdTensors* ts, float lr, float momentum, float dampening, float weight_decay,
+                           int nesterov, rplhip_stream_t stream) {
+    if (ts->count <= 0) return RPLHIP_OK;
+    if (ts->count > RPL_SGD_MULTI) return fail(RPLHIP_ERR_INVALID, "rplhip_sgd_step_multi: %d tensors", ts->count);
+    RPLHIP_REQUIRE_DEVICE();
+    uint32_t blocks = 0;
+    for (int k = 0; k < ts->count; k++) {
+        NEED(ts->p[k] && ts->g[k] && (momentum == 0.0f || ts->v[k]), "rplhip_sgd_step_multi");
+        ts->first[k] = blocks;
+        blocks += (uint32_t)grid_for(ts->n[k] ? ts->n[k] : 1);
+    }
+    ts->first[ts->count] = blocks;
+    hipLaunchKernelGGL(k_sgd_multi, dim3(blocks), dim3(kThreads), 0, as_stream(stream), *ts, lr, momentum, dampening,
+                       weight_decay, nesterov);
+    return check_launch("sgd_step_multi");
 }
 
 }  // extern "C"

@@ -149,6 +149,27 @@ Tensor* tensor_mse_loss(const Tensor* pred, const Tensor* target) {
 void backward_add(Tensor* t) {
     Tensor* a = t->parent1;
     Tensor* b = t->parent2;
+    if (a && a->grad && b && b->grad && rpl__is_gpu(t) && rpl__is_gpu(a) && rpl__is_gpu(b)) {
+        /* All on the device: one pass over dy writes a's gradient and the
+         * bias gradient's column partial sums, which are added into b's
+         * gradient after a's subgraph, in the reference's order. */
+        RplStage s = {0};
+        int ow_a = 0, ow_b = 0;
+        RplColsum cs = {0};
+        const float* dy = rpl__view_grad(&s, t, 1, 0);
+        float* da = rpl__view_grad_acc(&s, a, &ow_a);
+        if (!s.err)
+            s.err = !rpl__ok(rplhip__add_backward_begin(dy, t->size, da, ow_a, b->size, &cs, NULL), "backward_add");
+        rpl__stage_finish(&s);
+        if (a->backward_fn) a->backward_fn(a);
+        RplStage s2 = {0};
+        float* db = s.err ? NULL : rpl__view_grad_acc(&s2, b, &ow_b);
+        if (!rpl__ok(rplhip__add_backward_finish(&cs, s2.err ? NULL : db, ow_b, NULL), "backward_add (bias)"))
+            s2.err = 1;
+        rpl__stage_finish(&s2);
+        if (b->backward_fn) b->backward_fn(b);
+        return;
+    }
     if (a && a->grad) {
         RplStage s = {0};
         int ow = 0;
@@ -240,10 +261,12 @@ void backward_mse(Tensor* t) {
         int ow = 0;
         const float* dp = rpl__view_data(&s, pred, 1, 0);
         const float* dtg = rpl__view_data(&s, target, 1, 0);
-        const float* g0 = rpl__view_grad(&s, t, 1, 0);
+        /* The root gradient tensor_backward marks 1 goes in as a value. */
+        float g0v = 0.0f;
+        const float* g0 = t->size == 1 && rpl__grad_lazy_value(t, &g0v) ? NULL : rpl__view_grad(&s, t, 1, 0);
         float* dg = rpl__view_grad_acc(&s, pred, &ow);
         if (!s.err)
-            s.err = !rpl__ok(rplhip__mse_backward(dp, dtg, pred->size, g0, dg, ow, NULL), "backward_mse");
+            s.err = !rpl__ok(rplhip__mse_backward(dp, dtg, pred->size, g0, g0v, dg, ow, NULL), "backward_mse");
         rpl__stage_finish(&s);
         if (pred->backward_fn) pred->backward_fn(pred);
     }
@@ -258,9 +281,9 @@ void tensor_backward(Tensor* t) {
     }
     for (uint32_t i = 0; i < t->size; i++) t->grad[i] = 1.0f;
     if (rpl__is_gpu(t)) {
+        /* marked 1 everywhere, written only when read as an array */
         if (!rpl__attach_grad(t)) return;
-        rpl__grad_take_zero(t); /* overwritten by the fill */
-        if (!rpl__ok(rplhip_fill(rpl__dev_grad(t), t->size, 1.0f, NULL), "tensor_backward")) return;
+        rpl__grad_set_value(t, 1.0f);
     }
     if (t->backward_fn) t->backward_fn(t);
 }

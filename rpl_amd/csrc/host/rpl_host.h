@@ -40,14 +40,19 @@ int rpl__is_gpu(const Tensor* t);
  * root whose host gradient was created after it went to the device). */
 int rpl__attach_grad(Tensor* t);
 
-/* Device gradients are zeroed lazily: a new output's gradient, one attached
+/* Device gradients are filled lazily: a new output's gradient, one attached
  * by rpl__attach_grad and one cleared by tensor_zero_grad are only marked
- * zero.  The first accumulation into a marked gradient overwrites it
- * (0 + x, the same bits as accumulating into zeros); readers get it filled.
- * rpl__grad_take_zero tests and clears the mark, rpl__grad_set_zero sets it,
- * rpl__dev_grad_ready fills a marked gradient and returns it. */
+ * zero, tensor_backward's root is marked 1.  The first accumulation into a
+ * zero-marked gradient overwrites it (0 + x, the same bits as accumulating
+ * into zeros); readers, and accumulations into another value, get it
+ * filled.  rpl__grad_take_zero tests and clears a zero mark,
+ * rpl__grad_set_value / rpl__grad_set_zero set the mark,
+ * rpl__grad_lazy_value reads it, rpl__dev_grad_ready fills a marked
+ * gradient and returns it. */
 int rpl__grad_take_zero(const Tensor* t);
 void rpl__grad_set_zero(const Tensor* t);
+void rpl__grad_set_value(const Tensor* t, float v);
+int rpl__grad_lazy_value(const Tensor* t, float* v);
 float* rpl__dev_grad_ready(const Tensor* t);
 
 /* Staging of host tensors through device memory for one call. */

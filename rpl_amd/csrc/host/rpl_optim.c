@@ -66,6 +66,10 @@ Optimizer* optimizer_sgd_create(Tensor** parameters, uint32_t num_params, float 
 void optimizer_sgd_step(Optimizer* opt) {
     if (!opt || !opt->state) return;
     struct SGDState* st = (struct SGDState*)opt->state;
+    /* Device-resident parameters are updated RPL_SGD_MULTI per launch (the
+     * parameters are independent, so the order of launches does not matter). */
+    RplSgdTensors batch;
+    batch.count = 0;
     for (uint32_t p = 0; p < opt->num_params; p++) {
         Tensor* param = opt->parameters[p];
         if (!param || !param->grad) continue;
@@ -79,6 +83,26 @@ void optimizer_sgd_step(Optimizer* opt) {
             }
             if (rpl__is_gpu(param) && !rpl__is_gpu(v) && !rpl__attach(v, 1)) return;
         }
+        if (rpl__is_gpu(param) && (!v || rpl__is_gpu(v))) {
+            float* dg = rpl__dev_grad_ready(param);
+            if (!dg) {
+                rpl__bad("optimizer_sgd_step", "GPU parameter %u has no device gradient", p);
+                return;
+            }
+            const int k = batch.count++;
+            batch.p[k] = rpl__dev_data(param);
+            batch.g[k] = dg;
+            batch.v[k] = v ? rpl__dev_data(v) : NULL;
+            batch.n[k] = param->size;
+            if (batch.count == RPL_SGD_MULTI) {
+                if (!rpl__ok(rplhip__sgd_step_multi(&batch, opt->learning_rate, st->momentum, st->dampening,
+                                                    opt->weight_decay, st->nesterov, NULL),
+                             "optimizer_sgd_step"))
+                    return;
+                batch.count = 0;
+            }
+            continue;
+        }
         RplStage s = {0};
         float* dp = rpl__view_data(&s, param, 1, 1);
         float* dg = rpl__view_grad(&s, param, 1, 1);
@@ -89,4 +113,8 @@ void optimizer_sgd_step(Optimizer* opt) {
                              "optimizer_sgd_step");
         if (!rpl__stage_finish(&s)) return;
     }
+    if (batch.count)
+        rpl__ok(rplhip__sgd_step_multi(&batch, opt->learning_rate, st->momentum, st->dampening, opt->weight_decay,
+                                       st->nesterov, NULL),
+                "optimizer_sgd_step");
 }

@@ -114,7 +114,8 @@ typedef struct {
     float* grad;
     size_t bytes;
     int used;
-    int grad_zero; /* the device gradient is zero, not yet written (contents undefined) */
+    int grad_lazy;  /* the device gradient holds grad_val everywhere, not yet written (contents undefined) */
+    float grad_val;
 } RegEntry;
 
 enum { kRegChunkBits = 10, kRegChunk = 1 << kRegChunkBits, kRegMaxChunks = 4096 };
@@ -168,7 +169,8 @@ static uint32_t reg_new(float* data, float* grad, size_t bytes, int grad_zero) {
     e->grad = grad;
     e->bytes = bytes;
     e->used = 1;
-    e->grad_zero = grad_zero;
+    e->grad_lazy = grad_zero;
+    e->grad_val = 0.0f;
     pthread_mutex_unlock(&g_reg_mu);
     return h;
 }
@@ -262,7 +264,8 @@ int rpl__attach_grad(Tensor* t) {
         live = 1;
         if (!s->grad) {
             s->grad = g;
-            s->grad_zero = 1;
+            s->grad_lazy = 1;
+            s->grad_val = 0.0f;
             installed = 1;
         }
     }
@@ -271,37 +274,74 @@ int rpl__attach_grad(Tensor* t) {
     return live;
 }
 
-/* Test and clear the zero mark of t's device gradient: 1 if it was zero
- * only logically -- the caller then writes every element (as 0 + x). */
+/* Test and clear the zero mark of t's device gradient: 1 if it was +0.0
+ * only logically -- the caller then writes every element (as 0 + x).  A
+ * gradient marked with another value keeps its mark (0 returned). */
 int rpl__grad_take_zero(const Tensor* t) {
     if (!t || t->device != DEVICE_GPU) return 0;
     int was = 0;
     pthread_mutex_lock(&g_reg_mu);
     RegEntry* e = reg_slot(t->gpu_buffer);
-    if (e && e->grad && e->grad_zero) {
-        was = 1;
-        e->grad_zero = 0;
+    if (e && e->grad && e->grad_lazy) {
+        uint32_t bits;
+        memcpy(&bits, &e->grad_val, 4);
+        if (bits == 0) {
+            was = 1;
+            e->grad_lazy = 0;
+        }
     }
     pthread_mutex_unlock(&g_reg_mu);
     return was;
 }
 
-/* Mark t's device gradient zero without writing it (tensor_zero_grad). */
-void rpl__grad_set_zero(const Tensor* t) {
+/* Mark t's device gradient as holding v everywhere, without writing it
+ * (tensor_zero_grad: 0; tensor_backward's root: 1). */
+void rpl__grad_set_value(const Tensor* t, float v) {
     if (!t || t->device != DEVICE_GPU) return;
     pthread_mutex_lock(&g_reg_mu);
     RegEntry* e = reg_slot(t->gpu_buffer);
-    if (e && e->grad) e->grad_zero = 1;
+    if (e && e->grad) {
+        e->grad_lazy = 1;
+        e->grad_val = v;
+    }
     pthread_mutex_unlock(&g_reg_mu);
 }
 
-/* t's device gradient with its values in memory: a zero-marked gradient is
- * filled with zeros first.  NULL if t has none. */
+void rpl__grad_set_zero(const Tensor* t) { rpl__grad_set_value(t, 0.0f); }
+
+/* 1 (and *v) when t's device gradient holds one value only logically; the
+ * mark is kept. */
+int rpl__grad_lazy_value(const Tensor* t, float* v) {
+    if (!t || t->device != DEVICE_GPU) return 0;
+    int lazy = 0;
+    pthread_mutex_lock(&g_reg_mu);
+    RegEntry* e = reg_slot(t->gpu_buffer);
+    if (e && e->grad && e->grad_lazy) {
+        lazy = 1;
+        *v = e->grad_val;
+    }
+    pthread_mutex_unlock(&g_reg_mu);
+    return lazy;
+}
+
+/* Write a marked gradient's value into every element and clear the mark.
+ * 0 on a failed fill. */
+static int grad_materialize(const Tensor* t, float* g) {
+    float v;
+    if (!rpl__grad_lazy_value(t, &v)) return 1;
+    if (!rpl__ok(rplhip_fill(g, t->size, v, NULL), "device gradient")) return 0;
+    pthread_mutex_lock(&g_reg_mu);
+    RegEntry* e = reg_slot(t->gpu_buffer);
+    if (e) e->grad_lazy = 0;
+    pthread_mutex_unlock(&g_reg_mu);
+    return 1;
+}
+
+/* t's device gradient with its values in memory: a marked gradient is
+ * filled first.  NULL if t has none. */
 float* rpl__dev_grad_ready(const Tensor* t) {
     float* g = rpl__dev_grad(t);
-    if (g && rpl__grad_take_zero(t) &&
-        !rpl__ok(rplhip_fill(g, t->size, 0.0f, NULL), "device gradient"))
-        return NULL;
+    if (g && !grad_materialize(t, g)) return NULL;
     return g;
 }
 
@@ -362,7 +402,13 @@ float* rpl__view_grad_acc(RplStage* s, const Tensor* t, int* overwrite) {
             rpl__bad("autograd", "GPU tensor has no device gradient");
             return NULL;
         }
+        /* A zero mark becomes an overwrite; another value is written out
+         * first and then accumulated into. */
         *overwrite = rpl__grad_take_zero(t);
+        if (!*overwrite && !grad_materialize(t, g)) {
+            s->err = 1;
+            return NULL;
+        }
         return g;
     }
     return (float*)rpl__stage_host(s, t->grad, (size_t)t->size * sizeof(float), 1, 1);
@@ -543,11 +589,11 @@ void tensor_from_gpu(Tensor* t) {
     if (!rpl__ok(rplhip_memcpy_dtoh(t->data, d, bytes), "tensor_from_gpu")) return;
     float* g = rpl__dev_grad(t);
     if (!g || !t->grad) return;
-    if (rpl__grad_take_zero(t)) {
-        /* zero only logically: the host copy gets the zeros, the device
+    float v;
+    if (rpl__grad_lazy_value(t, &v)) {
+        /* one value only logically: the host copy gets it, the device
          * gradient keeps its mark */
-        memset(t->grad, 0, bytes);
-        rpl__grad_set_zero(t);
+        for (uint32_t i = 0; i < t->size; i++) t->grad[i] = v;
         return;
     }
     rpl__ok(rplhip_memcpy_dtoh(t->grad, g, bytes), "tensor_from_gpu (grad)");

@@ -20,9 +20,40 @@ extern "C" {
 int rplhip__accumulate(const float* dy, float* dx, uint64_t n, int overwrite, rplhip_stream_t stream);
 int rplhip__relu_backward(const float* x, const float* dy, float* dx, uint64_t n, int overwrite,
                           rplhip_stream_t stream);
-int rplhip__mse_backward(const float* pred, const float* target, uint64_t n, const float* g0, float* dpred,
-                         int overwrite, rplhip_stream_t stream);
+/* g0 NULL: the root gradient's value is g0_value. */
+int rplhip__mse_backward(const float* pred, const float* target, uint64_t n, const float* g0, float g0_value,
+                         float* dpred, int overwrite, rplhip_stream_t stream);
 int rplhip__bias_grad(const float* dy, uint64_t n, float* db, uint64_t nb, int overwrite, rplhip_stream_t stream);
+
+/* backward_add (src/rpl_core.c:319-337) of out = x + b[i % nb] in two
+ * steps that keep the reference's order -- x's gradient, x's subgraph,
+ * then b's gradient: _begin reads dy once, writing dx += dy (dx = 0 + dy
+ * with dx_overwrite) and the column partial sums of the bias gradient into
+ * a workspace held in *cs; _finish adds them into db (db = 0 + sum with
+ * db_overwrite; db NULL: just release) and releases the workspace.  The
+ * bits are those of rplhip__accumulate followed by rplhip__bias_grad. */
+typedef struct {
+    void* ws;
+    uint64_t splits, nb;
+} RplColsum;
+int rplhip__add_backward_begin(const float* dy, uint64_t n, float* dx, int dx_overwrite, uint64_t nb, RplColsum* cs,
+                               rplhip_stream_t stream);
+int rplhip__add_backward_finish(RplColsum* cs, float* db, int db_overwrite, rplhip_stream_t stream);
+
+/* rplhip_sgd_step for up to RPL_SGD_MULTI parameter tensors in one launch
+ * (optimizer_sgd_step's parameters are independent; the same bits as one
+ * launch each).  `first` is filled in by the call. */
+#define RPL_SGD_MULTI 8
+typedef struct {
+    float* p[RPL_SGD_MULTI];
+    float* g[RPL_SGD_MULTI];
+    float* v[RPL_SGD_MULTI];
+    uint64_t n[RPL_SGD_MULTI];
+    uint32_t first[RPL_SGD_MULTI + 1];
+    int count;
+} RplSgdTensors;
+int rplhip__sgd_step_multi(RplSgdTensors* ts, float lr, float momentum, float dampening, float weight_decay,
+                           int nesterov, rplhip_stream_t stream);
 
 /* linear_forward (src/rpl_nn.c:55-77) in one call: mm = X W^T (X [M,K],
  * W [N,K]; C written without being read, i.e. 1.0f * sum + 0.0f as

@@ -72,9 +72,13 @@ def _rel(got, want, scale):
 
 def mse_depth(n):
     """Longest chain of dependent adds in the device's MSE reduction
-    (linear.hip: k_sqerr_partial / k_sqerr_finish): a grid-stride sum per
-    thread over at most 1024 x 256 threads, a 64-lane butterfly (6 adds), 4
-    wave partials, then the same for <= 1024 block partials in one block."""
+    (linear.hip).  n <= 2^18, k_sqerr_single: a strided sum per thread over
+    1024 threads, a 64-lane butterfly (6 adds), the 16 wave sums in order.
+    Larger n, k_sqerr_partial / k_sqerr_finish: a grid-stride sum per thread
+    over at most 1024 x 256 threads, a 64-lane butterfly, 4 wave partials,
+    then the same for <= 1024 block partials in one block."""
+    if n <= 1 << 18:
+        return -(-n // 1024) + 6 + 16
     g = min(1024, max(1, (n + 255) // 256))
     per_thread = -(-n // (g * 256))
     return per_thread + 6 + 4 + -(-g // 256) + 6 + 4

@@ -85,6 +85,49 @@ def test_optimizer_sgd_rpl_api(gpu, golden, name, resident):
         lib.tensor_free(t)
 
 
+@pytest.mark.parametrize("mom,damp,wd,nest", [(0.0, 0.0, 0.0, False), (0.9, 0.1, 1e-2, True), (0.5, 0.0, 0.0, False)])
+def test_optimizer_sgd_many_params(gpu, orc, mom, damp, wd, nest):
+    # More parameters than one launch takes (eight device tensors per launch),
+    # of ragged sizes, with host-resident ones in between: every parameter
+    # bit for bit as the oracle's per-tensor update, over two steps.
+    lib = gpu
+    lr = 0.05
+    sizes = [1, 7, 256, 257, 1000, 65537, 3, 9, 1_200_000, 64, 5, 4097]
+    on_host = {3, 9}
+    ps, ref, vel = [], [], []
+    for k, n in enumerate(sizes):
+        a = rpl_amd.fill_uniform(n, seed(7, k), -1.0, 1.0)
+        t = tensor_from(lib, a, requires_grad=True)
+        if k not in on_host:
+            lib.tensor_to_gpu(t)
+        ps.append(t)
+        ref.append(a.copy())
+        vel.append(np.zeros(n, np.float32))
+    arr = (C.POINTER(rpl_amd.Tensor) * len(ps))(*ps)
+    opt = lib.optimizer_sgd_create(arr, len(ps), lr, mom, damp, wd, nest)
+    for step in range(2):
+        grads = []
+        for k, t in enumerate(ps):
+            gr = rpl_amd.fill_uniform(sizes[k], seed(8, 100 * step + k), -2.0, 2.0)
+            grads.append(gr)
+            C.memmove(t.contents.grad, gr.ctypes.data, gr.nbytes)
+            if k not in on_host:
+                rpl_amd.check(lib.rplhip_memcpy_htod(lib.rpl_tensor_device_grad(t), gr.ctypes.data, gr.nbytes))
+        say("sgd many params", mom, damp, wd, nest, "step", step)
+        lib.optimizer_sgd_step(opt)
+        err = lib.rpl_last_error()
+        assert not err, err
+        for k, t in enumerate(ps):
+            g = grads[k].copy()
+            orc.sgd_step(ref[k], g, vel[k] if mom else None, lr, mom, damp, wd, nest)
+            if k not in on_host:
+                lib.tensor_from_gpu(t)
+            assert bits_equal(host(t, (sizes[k],)), ref[k]), (step, k)
+            assert bits_equal(host(t, (sizes[k],), grad=True), g), (step, k)
+    for t in ps:
+        lib.tensor_free(t)
+
+
 def test_mlp_training_loop_on_device(gpu, orc):
     # Five steps of zero_grad / forward / backward / SGD with momentum, every
     # tensor GPU-resident, against the oracle's step + SGD on the same data.
