@@ -593,6 +593,286 @@ __global__ void __launch_bounds__(256) k_splitk_reduce(const float* __restrict__
 
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
+// ----------------------------------------- wave-split kernel (small grids)
+//
+// For products whose 128 x 128 tiles leave most CUs idle (the MLP's
+// 4096 x 128 x 784 forward product, its 128 x 784 x 4096 and 10 x 128 x 4096
+// weight gradients).  One block per (16 FM) x 64 output tile and K range; each
+// of its 4 waves multiplies the WHOLE tile over a quarter of the block's K
+// range, loading its operands from global memory straight into registers (no
+// LDS and no barrier in the k loop), P steps of 16 k in flight.  The waves'
+// partial tiles are then added in LDS in wave order, so the result does not
+// depend on timing.  A K range split over several blocks (nsplit > 1) writes
+// raw partial tiles W[split] ([M, N], ld N) for k_splitk_reduce; otherwise the
+// block applies alpha, beta and the bias itself, as k_splitk_reduce does.
+#ifndef RPL_WS_WAVES
+#define RPL_WS_WAVES 4
+#endif
+#ifndef RPL_WS_PREFETCH
+#define RPL_WS_PREFETCH 3
+#endif
+namespace wsk {
+constexpr int kWaves = RPL_WS_WAVES, kThreads = 64 * kWaves, FN = 4, BN = 16 * FN, P = RPL_WS_PREFETCH;
+
+// One operand of a wave's 16-k step.  KC: stored [rows, K] (k contiguous),
+// else [K, rows].  F = the wave's MFMA blocks along this operand.  v[f][s] is
+// what this lane feeds block f at substep s, whose k is k0 + 4 (lane / 16) + s
+// for every lane group (so A and B agree).  Addresses are clamped into the
+// matrix: a row past `rows` only feeds output rows or columns that are never
+// stored, and a k past K only prefetched steps that are never multiplied, so
+// the k loop takes the values as loaded (a select or a branch per load made
+// the compiler wait for each load at once).  MASK zeroes k >= K, for the one
+// partial step at the end of K.
+template <bool KC, int F>
+struct WaveOp {
+    const float* __restrict__ base;
+    uint32_t ld, rows, K;
+
+    template <bool MASK>
+    __device__ __forceinline__ void load(uint32_t r0, uint32_t k0, uint32_t lane, float v[F][4]) const {
+        const uint32_t g = lane / 16, li = lane % 16;
+        if (KC) {
+            // block f, in-block row li = tile row 16 f + li; 4 consecutive k
+            // (K % 4 == 0)
+            const uint32_t k = k0 + 4 * g, kc = k < K ? k : K - 4;
+#pragma unroll
+            for (int f = 0; f < F; f++) {
+                const uint32_t r = r0 + 16 * f + li, rc = r < rows ? r : rows - 1;
+                const float4 x = *reinterpret_cast<const float4*>(base + (uint64_t)rc * ld + kc);
+                const bool ok = !MASK || k < K;
+                v[f][0] = ok ? x.x : 0.f;
+                v[f][1] = ok ? x.y : 0.f;
+                v[f][2] = ok ? x.z : 0.f;
+                v[f][3] = ok ? x.w : 0.f;
+            }
+        } else {
+            // k-row k0 + 4g + s; F consecutive rows F li .. F li + F - 1, row
+            // F li + f being block f's in-block row li (rows % F == 0)
+            const uint32_t r = r0 + F * li, rc = r < rows ? r : rows - F;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const uint32_t k = k0 + 4 * g + s, kc = k < K ? k : K - 1;
+                const bool ok = !MASK || k < K;
+                const float* p = base + (uint64_t)kc * ld + rc;
+                if (F == 4) {
+                    const float4 x = *reinterpret_cast<const float4*>(p);
+                    v[0][s] = ok ? x.x : 0.f;
+                    v[1 % F][s] = ok ? x.y : 0.f;
+                    v[2 % F][s] = ok ? x.z : 0.f;
+                    v[3 % F][s] = ok ? x.w : 0.f;
+                } else if (F == 2) {
+                    const float2 x = *reinterpret_cast<const float2*>(p);
+                    v[0][s] = ok ? x.x : 0.f;
+                    v[1 % F][s] = ok ? x.y : 0.f;
+                } else {
+                    const float x = *p;
+                    v[0][s] = ok ? x : 0.f;
+                }
+            }
+        }
+    }
+
+    // Tile-relative row of block f's in-block row i.
+    __device__ __forceinline__ static uint32_t row_of(int f, uint32_t i) { return KC ? 16 * f + i : F * i + f; }
+};
+
+template <bool TA, bool TB, int FM, bool SPLIT>
+__global__ void __launch_bounds__(kThreads) k_sgemm_ws(uint32_t M, uint32_t N, uint32_t K, float alpha,
+                                                       const float* __restrict__ A, uint32_t lda,
+                                                       const float* __restrict__ B, uint32_t ldb, float beta,
+                                                       float* __restrict__ C, uint32_t ldc, int read_c,
+                                                       const float* __restrict__ bias, float* __restrict__ out2,
+                                                       uint32_t tiles_m, uint32_t tiles_n, uint32_t spb) {
+    constexpr int BM = 16 * FM, kPitch = BN + 4;
+    using OpA = WaveOp<!TA, FM>;
+    using OpB = WaveOp<TB, FN>;
+    __shared__ __attribute__((aligned(16))) float red[kWaves][BM * kPitch];
+
+    // Blocks b, b + 8, b + 16, ... run on one XCD: give them consecutive
+    // (split, tile m, tile n) so that they share operand panels in its L2.
+    const uint32_t total = gridDim.x, full = total / 8 * 8;
+    uint32_t lin = blockIdx.x < full ? (blockIdx.x % 8) * (full / 8) + blockIdx.x / 8 : blockIdx.x;
+    const uint32_t tn = lin % tiles_n;
+    lin /= tiles_n;
+    const uint32_t tm = lin % tiles_m, sp = lin / tiles_m;
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+
+    const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const uint32_t steps = (K + 15) / 16;
+    const uint32_t b0 = sp * spb, b1 = b0 + spb < steps ? b0 + spb : steps;
+    const uint32_t spw = (b1 - b0 + kWaves - 1) / kWaves;
+    const uint32_t w0 = b0 + wave * spw < b1 ? b0 + wave * spw : b1;
+    const uint32_t w1 = w0 + spw < b1 ? w0 + spw : b1;
+    const uint32_t kbeg = 16 * w0, kend = 16 * w1 < K ? 16 * w1 : K;
+    const int n = (int)(w1 - w0);
+
+    const OpA opa{A, lda, M, K};
+    const OpB opb{B, ldb, N, K};
+    v4f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    float a[P][FM][4], b[P][FN][4];
+    auto load = [&](int slot, int t) {
+        opa.template load<false>(m0, kbeg + 16 * t, lane, a[slot]);
+        opb.template load<false>(n0, kbeg + 16 * t, lane, b[slot]);
+    };
+    auto step = [&](int slot) {
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[slot][i][s], b[slot][j][s], acc[i][j], 0, 0, 0);
+    };
+    // Full steps in a ring of P slots; prefetches past them are never
+    // multiplied, so the loop body needs no condition.  A partial last step
+    // (K % 16 != 0, the last wave with steps) is loaded again masked.
+    const bool partial = n > 0 && (kend & 15) != 0;
+    const int nf = n - (partial ? 1 : 0);
+#pragma unroll
+    for (int u = 0; u < P; u++) load(u, u);
+    int t = 0;
+    for (; t + P <= nf; t += P) {
+#pragma unroll
+        for (int u = 0; u < P; u++) {
+            // Kept in this order: slot u's refill issued right after its
+            // multiplies, so the loads complete in slot order and the wait
+            // before slot u + 1 leaves 2 slots' loads in flight.
+            step(u);
+            __builtin_amdgcn_sched_barrier(0);
+            load(u, t + u + P);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < P - 1; u++)
+        if (nf - t > u) step(u);
+    if (partial) {
+        opa.template load<true>(m0, kbeg + 16 * nf, lane, a[0]);
+        opb.template load<true>(n0, kbeg + 16 * nf, lane, b[0]);
+        step(0);
+    }
+
+    // Partial tiles into LDS; then each thread adds the four waves' values of
+    // 4 consecutive columns, in wave order.
+    const uint32_t g = lane / 16, li = lane % 16;
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                red[wave][OpA::row_of(i, 4 * g + r) * kPitch + OpB::row_of(j, li)] = acc[i][j][r];
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < (uint32_t)(BM * BN / 4); e += kThreads) {
+        const uint32_t row = e / (BN / 4), col = 4 * (e % (BN / 4));
+        const uint32_t m = m0 + row, nn = n0 + col;
+        if (m >= M || nn >= N) continue;  // N % 4 == 0: a column group is all in or all out
+        float4 sum = *reinterpret_cast<const float4*>(&red[0][row * kPitch + col]);
+#pragma unroll
+        for (int w = 1; w < kWaves; w++) {
+            const float4 x = *reinterpret_cast<const float4*>(&red[w][row * kPitch + col]);
+            sum.x += x.x;
+            sum.y += x.y;
+            sum.z += x.z;
+            sum.w += x.w;
+        }
+        if (SPLIT) {
+            *reinterpret_cast<float4*>(&C[(uint64_t)sp * M * N + (uint64_t)m * N + nn]) = sum;
+        } else {
+            float* cp = &C[(uint64_t)m * ldc + nn];
+            float4 c = read_c ? *reinterpret_cast<const float4*>(cp) : make_float4(0.f, 0.f, 0.f, 0.f);
+            c.x = alpha * sum.x + (read_c ? beta * c.x : 0.0f);
+            c.y = alpha * sum.y + (read_c ? beta * c.y : 0.0f);
+            c.z = alpha * sum.z + (read_c ? beta * c.z : 0.0f);
+            c.w = alpha * sum.w + (read_c ? beta * c.w : 0.0f);
+            *reinterpret_cast<float4*>(cp) = c;
+            if (bias) {
+                const float4 bv = *reinterpret_cast<const float4*>(&bias[nn]);
+                *reinterpret_cast<float4*>(&out2[(uint64_t)m * ldc + nn]) =
+                    make_float4(c.x + bv.x, c.y + bv.y, c.z + bv.z, c.w + bv.w);
+            }
+        }
+    }
+}
+
+// Steps of 16 k per wave below which a K split over blocks is not worth its
+// partial tiles.
+constexpr uint32_t kMinWaveSteps = 4;
+
+template <bool TA, bool TB, int FM>
+int launch_fm(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint32_t lda, const float* B,
+              uint32_t ldb, float beta, float* C, uint32_t ldc, hipStream_t s, int read_c, const float* bias,
+              float* out2) {
+    const uint32_t tiles_m = (M + 16 * FM - 1) / (16 * FM), tiles_n = (N + BN - 1) / BN;
+    const uint64_t tiles = (uint64_t)tiles_m * tiles_n;
+    const uint32_t steps = (K + 15) / 16;
+    uint64_t ns = rplhip::cu_count() / tiles;
+    const uint64_t cap = steps / (kWaves * kMinWaveSteps);
+    if (ns > cap) ns = cap;
+    if (ns < 1) ns = 1;
+    const uint32_t spb = (uint32_t)((steps + ns - 1) / ns);
+    ns = spb ? (steps + spb - 1) / spb : 1;
+    if (ns < 1) ns = 1;
+    if (tiles * ns > 0x7fffffffull) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "sgemm: %u x %u too large", M, N);
+    const dim3 grid((uint32_t)(tiles * ns));
+    if (ns == 1) {
+        hipLaunchKernelGGL((k_sgemm_ws<TA, TB, FM, false>), grid, dim3(kThreads), 0, s, M, N, K, alpha, A, lda, B, ldb,
+                           beta, C, ldc, read_c, bias, out2, tiles_m, tiles_n, spb);
+        return rplhip::check_launch("sgemm (wave split)");
+    }
+    void* ws = nullptr;
+    int st = rplhip::ws_alloc(&ws, (size_t)ns * M * N * sizeof(float), s);
+    if (st) return st;
+    hipLaunchKernelGGL((k_sgemm_ws<TA, TB, FM, true>), grid, dim3(kThreads), 0, s, M, N, K, 1.0f, A, lda, B, ldb,
+                       0.0f, (float*)ws, N, 0, nullptr, nullptr, tiles_m, tiles_n, spb);
+    st = rplhip::check_launch("sgemm (wave split)");
+    if (!st) {
+        const uint64_t total = (uint64_t)M * N;
+        hipLaunchKernelGGL(k_splitk_reduce, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, (const float*)ws,
+                           (uint32_t)ns, M, N, alpha, beta, C, ldc, read_c, bias, out2);
+        st = rplhip::check_launch("sgemm (wave split reduction)");
+    }
+    rplhip::ws_free(ws, s);
+    return st;
+}
+
+bool aligned(const void* p, uintptr_t bytes) { return (((uintptr_t)p) % bytes) == 0; }
+
+// Whether an operand suits WaveOp<KC, F>'s vector loads.
+bool operand_ok(bool kc, int f, const float* p, uint32_t ld, uint32_t rows, uint32_t K) {
+    return kc ? aligned(p, 16) && ld % 4 == 0 && K % 4 == 0 : aligned(p, 4 * f) && ld % f == 0 && rows % f == 0;
+}
+
+// Tile height: the largest of 64 / 32 / 16 rows whose tiles fill the CUs
+// without a K split; else 64 rows (16 or 32 for short M).  Returns -1, having
+// launched nothing, when the operands do not suit the kernel's vector
+// accesses.
+template <bool TA, bool TB>
+int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint32_t lda, const float* B,
+           uint32_t ldb, float beta, float* C, uint32_t ldc, hipStream_t s, int read_c, const float* bias,
+           float* out2) {
+    const uint64_t tn = (N + BN - 1) / BN, cu = rplhip::cu_count();
+    int fm = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+    if ((M + 63) / 64 * tn < cu) {
+        if ((M + 31) / 32 * tn >= cu)
+            fm = 2;
+        else if ((M + 15) / 16 * tn >= cu)
+            fm = 1;
+    }
+    if (!operand_ok(!TA, fm, A, lda, M, K) || !operand_ok(TB, FN, B, ldb, N, K) || !aligned(C, 16) || ldc % 4 ||
+        N % 4 || (bias && (!aligned(bias, 16) || !aligned(out2, 16))))
+        return -1;
+    if (fm == 1) return launch_fm<TA, TB, 1>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s, read_c, bias, out2);
+    if (fm == 2) return launch_fm<TA, TB, 2>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s, read_c, bias, out2);
+    return launch_fm<TA, TB, 4>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s, read_c, bias, out2);
+}
+}  // namespace wsk
+
 // K splits for a grid of `tiles` tiles: enough blocks to fill the CUs twice,
 // each split at least RPL_F32_MIN_KSPLIT long (a multiple of BK); 1 = no
 // split.  Measured minimum lengths 256 / 128 / 64: config 0 (512^3) 27.0 /
@@ -614,7 +894,10 @@ uint32_t k_splits(uint64_t tiles, uint32_t K) {
 // The operation order is src/rpl_core.c:208-213's: sum = fma(a, b, sum) over
 // k in order, then C = fma(alpha, sum, beta * C) (GCC's contraction of
 // alpha*sum + beta*C), so these outputs equal the reference's bit for bit.
-template <bool TA, bool TB>
+// V4 (A as [M,K] and B as [N,K], 16-byte aligned rows): the same fma chain
+// fed by 128-bit loads, 8 of each in flight (the scalar loads left the
+// 4096 x 10 x 128 product latency-bound).
+template <bool TA, bool TB, bool V4>
 __global__ void __launch_bounds__(256) k_sgemm_valu(uint32_t M, uint32_t N, uint32_t K, float alpha,
                                                     const float* __restrict__ A, uint32_t lda,
                                                     const float* __restrict__ B, uint32_t ldb, float beta,
@@ -624,8 +907,23 @@ __global__ void __launch_bounds__(256) k_sgemm_valu(uint32_t M, uint32_t N, uint
     if (i >= (uint64_t)M * N) return;
     const uint32_t m = (uint32_t)(i / N), n = (uint32_t)(i % N);
     float sum = 0.0f;
+    uint32_t k0 = 0;
+    if constexpr (V4) {
+        static_assert(!TA && TB, "V4 reads both operands along k");
+        const float4* a4 = reinterpret_cast<const float4*>(A + (uint64_t)m * lda);
+        const float4* b4 = reinterpret_cast<const float4*>(B + (uint64_t)n * ldb);
 #pragma unroll 8
-    for (uint32_t k = 0; k < K; k++) {
+        for (uint32_t q = 0; q < K / 4; q++) {
+            const float4 a = a4[q], b = b4[q];
+            sum = __builtin_fmaf(a.x, b.x, sum);
+            sum = __builtin_fmaf(a.y, b.y, sum);
+            sum = __builtin_fmaf(a.z, b.z, sum);
+            sum = __builtin_fmaf(a.w, b.w, sum);
+        }
+        k0 = K / 4 * 4;
+    }
+#pragma unroll 8
+    for (uint32_t k = k0; k < K; k++) {
         const float a = TA ? A[(uint64_t)k * lda + m] : A[(uint64_t)m * lda + k];
         const float b = TB ? B[(uint64_t)n * ldb + k] : B[(uint64_t)k * ldb + n];
         sum = __builtin_fmaf(a, b, sum);
@@ -677,10 +975,27 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
                ldc % 4 == 0 && N % 4 == 0 && (TA ? M % 4 == 0 : K % 4 == 0) && (TB ? K % 4 == 0 : true);
     const uint64_t tiles = (uint64_t)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
     if (tiles > 0x7fffffffull) return rplhip::fail(RPLHIP_ERR_UNSUPPORTED, "sgemm: %u x %u too large", M, N);
-    if (K > 0 && K <= kValuMaxK && (uint64_t)M * N * K <= kValuMaxWork) {
+    const bool valu = K > 0 && K <= kValuMaxK && (uint64_t)M * N * K <= kValuMaxWork;
+    // Small grids (a K split of the 128 x 128 tiles, or the VALU split) on
+    // the wave-split kernel when the operands suit its vector accesses
+    // (RPLHIP_F32_WS=0 disables it, for A/B timing only).
+    static const char* ws_env = getenv("RPLHIP_F32_WS");
+    if (!valu && K > 0 && !(ws_env && ws_env[0] == '0') &&
+        ((uint64_t)M * N * K <= kValuMaxWork || k_splits(tiles, K) > 1)) {
+        const int st = wsk::launch<TA, TB>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s, read_c, bias, out2);
+        if (st != -1) return st;
+    }
+    if (valu) {
         const uint64_t blocks = ((uint64_t)M * N + 255) / 256;  // M*N <= 2^23
-        hipLaunchKernelGGL((k_sgemm_valu<TA, TB>), dim3((uint32_t)blocks), dim3(256), 0, s, M, N, K, alpha, A, lda, B,
-                           ldb, beta, C, ldc, read_c, bias, out2);
+        if constexpr (!TA && TB) {
+            if (aligned16(A) && aligned16(B) && lda % 4 == 0 && ldb % 4 == 0) {
+                hipLaunchKernelGGL((k_sgemm_valu<false, true, true>), dim3((uint32_t)blocks), dim3(256), 0, s, M, N,
+                                   K, alpha, A, lda, B, ldb, beta, C, ldc, read_c, bias, out2);
+                return rplhip::check_launch("sgemm (VALU)");
+            }
+        }
+        hipLaunchKernelGGL((k_sgemm_valu<TA, TB, false>), dim3((uint32_t)blocks), dim3(256), 0, s, M, N, K, alpha, A,
+                           lda, B, ldb, beta, C, ldc, read_c, bias, out2);
         return rplhip::check_launch("sgemm (VALU)");
     }
     if (K > kValuMaxK && (uint64_t)M * N * K <= kValuMaxWork) {

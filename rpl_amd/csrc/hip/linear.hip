@@ -191,8 +191,9 @@ __global__ void __launch_bounds__(kThreads) k_sqerr_finish(const float* __restri
 }
 
 // n <= kSqerrSingleMax: the whole sum in one block (one launch instead of
-// partials plus a finishing block): a strided sum per thread, a 64-lane
-// butterfly, then the 16 wave sums in order.
+// partials plus a finishing block): a strided sum per thread (4 consecutive
+// elements per step when aligned), a 64-lane butterfly, then the 16 wave sums
+// in order.
 constexpr int kSqerrThreads = 1024;
 constexpr uint64_t kSqerrSingleMax = uint64_t(1) << 18;
 __global__ void __launch_bounds__(kSqerrThreads) k_sqerr_single(const float* __restrict__ p,
@@ -200,8 +201,25 @@ __global__ void __launch_bounds__(kSqerrThreads) k_sqerr_single(const float* __r
                                                                 float* __restrict__ loss) {
     __shared__ float s[kSqerrThreads / 64];
     float acc = 0;
-#pragma unroll 8
-    for (uint64_t i = threadIdx.x; i < n; i += kSqerrThreads) {
+    uint64_t i0 = 0;
+    if ((((uintptr_t)p | (uintptr_t)t) & 15) == 0) {
+        // 128-bit loads over the first n - n % 4 elements (more loads in
+        // flight per thread: the single block is latency-bound)
+        const uint64_t n4 = n / 4;
+        const float4* p4 = reinterpret_cast<const float4*>(p);
+        const float4* t4 = reinterpret_cast<const float4*>(t);
+#pragma unroll 4
+        for (uint64_t i = threadIdx.x; i < n4; i += kSqerrThreads) {
+            const float4 a = p4[i], b = t4[i];
+            const float d0 = a.x - b.x, d1 = a.y - b.y, d2 = a.z - b.z, d3 = a.w - b.w;
+            acc += d0 * d0;
+            acc += d1 * d1;
+            acc += d2 * d2;
+            acc += d3 * d3;
+        }
+        i0 = 4 * n4;
+    }
+    for (uint64_t i = i0 + threadIdx.x; i < n; i += kSqerrThreads) {
         const float d = p[i] - t[i];
         acc += d * d;
     }

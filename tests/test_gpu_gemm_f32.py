@@ -56,8 +56,23 @@ def test_sgemm_small_vs_oracle(gpu, orc, M, N, K, ta, tb):
         ref = orc.sgemm(A, B, C0, M, N, K, alpha, beta, bool(ta), bool(tb))
         if K <= 256:
             assert bits_equal(out, ref)
-        else:  # (10, 128, 300): K past the single-pass bound, summed in k slices (VALU split-K)
+        else:  # (10, 128, 300): K past the single-pass bound (wave-split kernel, or VALU k slices)
             assert gemm_err_ratio(out, op(A, ta), op(B, tb), ref, alpha, beta, C0) <= fp32_tol(K)
+
+
+def test_sgemm_small_padded_rows_bit_exact(gpu, orc):
+    # A as [M,K] and B as [N,K] with 16-byte aligned rows (lda = ldb = 132)
+    # and K % 4 == 2: 128-bit loads for k < 128, then two scalar steps; the
+    # fma chain is the reference's either way.
+    rng = np.random.default_rng(11)
+    M, N, K, ld = 64, 16, 130, 132
+    Abig = rng.uniform(-1, 1, (M, ld)).astype(np.float32)
+    Bbig = rng.uniform(-1, 1, (N, ld)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+    say("sgemm small padded rows")
+    out = sgemm(Abig, Bbig, C0, M, N, K, 0.75, -0.5, 0, 1, lda=ld, ldb=ld)
+    ref = orc.sgemm(Abig[:, :K].copy(), Bbig[:, :K].copy(), C0, M, N, K, 0.75, -0.5, False, True)
+    assert bits_equal(out, ref)
 
 
 def test_sgemm_nan_in_c_propagates(gpu, golden):
@@ -97,9 +112,10 @@ def test_sgemm_known_answers(gpu):
     assert np.array_equal(sgemm(A, np.eye(256, dtype=np.float32), np.zeros_like(A), 256, 256, 256), A)
 
 
-# (17, 33, 2049), (128, 784, 4096), (10, 128, 4096) and (512, 512, 512) take
-# the split-K path (few 128 x 128 tiles, long K): partial tiles in a
-# workspace, then C = alpha * sum + beta * C.
+# (17, 33, 2049) takes the split-K path of the 128 x 128 kernel (few tiles,
+# long K, N % 4 != 0): partial tiles in a workspace, then
+# C = alpha * sum + beta * C; (128, 784, 4096), (10, 128, 4096) and
+# (512, 512, 512) the wave-split kernel.
 SHAPES = [(1, 1, 1), (3, 5, 7), (127, 129, 65), (130, 7, 300), (64, 256, 32), (200, 130, 1), (17, 33, 2049),
           (256, 256, 0), (128, 784, 4096), (10, 128, 4096), (512, 512, 512)]
 
@@ -115,6 +131,38 @@ def test_sgemm_ragged_vs_oracle(gpu, orc, M, N, K, ta, tb):
     out = sgemm(A, B, C0, M, N, K, 1.25, 0.5, ta, tb)
     ref = orc.sgemm(A, B, C0, M, N, K, 1.25, 0.5, bool(ta), bool(tb))
     assert gemm_err_ratio(out, op(A, ta), op(B, tb), ref, 1.25, 0.5, C0) <= fp32_tol(K)
+
+
+# Small grids (a K split of the 128 x 128 tiles, or K > 256 with
+# M*N*K <= 2^23) on the wave-split kernel, 128-bit shapes only: tiles of
+# 16 / 32 / 64 rows x 64 columns, four waves per tile each over a quarter of
+# the block's K range, K split over blocks when the tiles are few.  Shapes
+# cover each tile height, a partial last 16-k step (K % 16 != 0), columns
+# and rows past the matrix in edge tiles, no split / a few / 256 splits, the
+# MLP's three products, and operands the kernel does not take (K % 4 != 0
+# with a k-contiguous operand: the older paths).  A NaN in C stays where it
+# is (C is read).
+WS_SHAPES = [(4096, 128, 784), (4096, 128, 792), (128, 784, 4096), (10, 128, 4096), (12, 128, 4100),
+             (36, 68, 1000), (1000, 100, 300), (512, 512, 512), (64, 64, 65536), (20, 8, 260), (16, 64, 1025)]
+
+
+@pytest.mark.parametrize("M,N,K", WS_SHAPES)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_wave_split_vs_float64(gpu, M, N, K, ta, tb):
+    rng = np.random.default_rng(M * 7 + N * 3 + K + 2 * ta + tb)
+    A = rng.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (N, K) if tb else (K, N)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+    C0[M // 2, N // 3] = np.nan
+    alpha, beta = 0.75, -0.5
+    say("sgemm wave split", M, N, K, ta, tb)
+    out = sgemm(A, B, C0, M, N, K, alpha, beta, ta, tb)
+    assert np.isnan(out[M // 2, N // 3]) and np.isnan(out).sum() == 1
+    opA, opB = op(A, ta).astype(np.float64), op(B, tb).astype(np.float64)
+    ref = alpha * (opA @ opB) + beta * C0.astype(np.float64)
+    ok = ~np.isnan(ref)
+    assert gemm_err_ratio(np.where(ok, out, 0), op(A, ta), op(B, tb), np.where(ok, ref, 0), alpha, beta,
+                          np.nan_to_num(C0)) <= fp32_tol(K)
 
 
 def test_sgemm_leading_dimensions(gpu, orc):

@@ -73,12 +73,14 @@ def _rel(got, want, scale):
 def mse_depth(n):
     """Longest chain of dependent adds in the device's MSE reduction
     (linear.hip).  n <= 2^18, k_sqerr_single: a strided sum per thread over
-    1024 threads, a 64-lane butterfly (6 adds), the 16 wave sums in order.
+    1024 threads (4 consecutive elements per step), a 64-lane butterfly (6
+    adds), the 16 wave sums in order.
     Larger n, k_sqerr_partial / k_sqerr_finish: a grid-stride sum per thread
     over at most 1024 x 256 threads, a 64-lane butterfly, 4 wave partials,
     then the same for <= 1024 block partials in one block."""
     if n <= 1 << 18:
-        return -(-n // 1024) + 6 + 16
+        # 128-bit loop: 4 adds per 4096 elements; then at most one remainder add
+        return 4 * -(-n // 4096) + 1 + 6 + 16
     g = min(1024, max(1, (n + 255) // 256))
     per_thread = -(-n // (g * 256))
     return per_thread + 6 + 4 + -(-g // 256) + 6 + 4
@@ -261,6 +263,25 @@ def test_bias_pieces_vs_oracle(gpu, orc, n, nb):
     say("relu_backward", n)
     rpl_amd.check(lib.rplhip_relu_backward(dmm.ptr, ddy.ptr, ddx.ptr, n, None))
     assert np.array_equal(down(ddx, np.float32, (n,)), orc.relu_backward(mm, dy, dx0))
+
+
+@pytest.mark.parametrize("n,off", [(1, 0), (3, 0), (5, 1), (4097, 0), (4099, 1), (1 << 18, 0), (1 << 18, 1),
+                                   ((1 << 18) + 1, 0), (1 << 20, 0)])
+def test_mse_loss_sizes(gpu, n, off):
+    # One block up to 2^18 elements (128-bit loads when both inputs are
+    # 16-byte aligned, `off` = 1 float misaligns them), partials beyond.
+    lib = gpu
+    rng = np.random.default_rng(n + off)
+    p = rng.standard_normal(n + off).astype(np.float32)
+    t = rng.standard_normal(n + off).astype(np.float32)
+    dp, dt, dl = up(p), up(t), empty(1, np.float32)
+    say("mse sizes", n, off)
+    rpl_amd.check(lib.rplhip_mse_loss(C.c_void_p(dp.ptr.value + 4 * off), C.c_void_p(dt.ptr.value + 4 * off), n,
+                                      dl.ptr, None))
+    loss = down(dl, np.float32, (1,))[0]
+    d64 = p[off:].astype(np.float64) - t[off:]
+    exact = float(np.mean(d64 * d64))
+    assert abs(float(loss) - exact) <= (mse_depth(n) + 4) * 2.0 ** -24 * exact
 
 
 def test_mse_vs_oracle(gpu, orc):
