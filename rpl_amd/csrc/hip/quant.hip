@@ -239,26 +239,42 @@ __device__ __forceinline__ uint32_t pack4(uint32_t b0, uint32_t b1, uint32_t b2,
     return __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u) | __builtin_amdgcn_perm(b3, b2, 0x04000c0cu);
 }
 
-// k_quantize_rows_wave: one wave per slice of up to 256*NV floats (cols % 4
-// == 0, 16-byte aligned rows), 4 slices per block.  Lane l holds float4
-// items l, l+64, .. in registers, so the slice is read from HBM once; every
-// load is unconditional (items past the slice re-read its last float4, which
-// leaves the largest |x| unchanged) so all NV loads are in flight together,
-// and the reduction is wave-local (no LDS, no block barrier).  FULL: the
-// slice is exactly 256*NV floats (no item is past it).
-template <int NV, bool FULL>
+// k_quantize_rows_wave: WPR waves per slice of up to 256*NV*WPR floats
+// (cols % 4 == 0, 16-byte aligned rows), 4/WPR slices per block.  Lane l of
+// the slice's 64*WPR lanes holds float4 items l, l + 64 WPR, .. in
+// registers, so the slice is read from HBM once; every load is unconditional
+// (items past the slice re-read its last float4, which leaves the largest
+// |x| unchanged) so all NV loads are in flight together.  The reduction is
+// wave-local, then across the slice's waves through LDS when WPR > 1.  FULL:
+// the slice is exactly 256*NV*WPR floats.  NT: non-temporal loads (X is read
+// once).  Measured on 2048 x 4096 (config 3's tokens): one wave per row,
+// 11.5 us with X in HBM (6.7 us from the MALL); 4 waves per row with NT
+// loads, 8.5 us (6.6 us); 2 or 8 waves, or NT loads with one wave, in between.
+template <int NV, int WPR, bool FULL, bool NT>
 __global__ void __launch_bounds__(kThreads) k_quantize_rows_wave(const float* __restrict__ x, uint32_t rows,
                                                                  uint32_t cols, int8_t* __restrict__ q,
                                                                  float* __restrict__ scales) {
-    const uint32_t r = blockIdx.x * (kThreads / 64) + threadIdx.x / 64;
-    if (r >= rows) return;
-    const uint32_t lane = threadIdx.x % 64, n4 = cols / 4;
-    const float4* x4 = reinterpret_cast<const float4*>(x + (uint64_t)r * cols);
+    static_assert(kThreads == 256 && 4 % WPR == 0, "4 waves per block, WPR of them per slice");
+    constexpr uint32_t T = 64 * WPR;
+    const uint32_t r = blockIdx.x * (4 / WPR) + threadIdx.x / T;
+    // With WPR == 1 a wave past the last slice leaves at once; with WPR > 1
+    // the grid has exactly one block per slice group (rows % (4 / WPR) is
+    // handled by `live`), so every wave reaches the barrier.
+    const bool live = r < rows;
+    if (WPR == 1 && !live) return;
+    const uint32_t lane = threadIdx.x % T, n4 = cols / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(x + (uint64_t)(live ? r : 0) * cols);
     float4 v[NV];
 #pragma unroll
     for (int it = 0; it < NV; it++) {
-        const uint32_t i = lane + 64 * it;
-        v[it] = x4[FULL || i < n4 ? i : n4 - 1];
+        const uint32_t i = lane + T * it;
+        const float4* p = x4 + (FULL || i < n4 ? i : n4 - 1);
+        if (NT) {
+            const v4f t = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p));
+            v[it] = make_float4(t[0], t[1], t[2], t[3]);
+        } else {
+            v[it] = *p;
+        }
     }
     // Largest |x| over non-NaN elements (fmaxf returns the other operand
     // for a NaN); -1 when there is none.
@@ -270,14 +286,25 @@ __global__ void __launch_bounds__(kThreads) k_quantize_rows_wave(const float* __
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) amax = __builtin_fmaxf(__shfl_xor(amax, off), amax);
+    if constexpr (WPR > 1) {
+        __shared__ float red[4];
+        const uint32_t w = threadIdx.x / 64;
+        if (threadIdx.x % 64 == 0) red[w] = amax;
+        __syncthreads();
+        const uint32_t w0 = w / WPR * WPR;
+        amax = red[w0];
+#pragma unroll
+        for (int i = 1; i < WPR; i++) amax = __builtin_fmaxf(amax, red[w0 + i]);
+        if (!live) return;
+    }
     const float scale = (amax < 0.0f ? FLT_MAX : amax) / 127.0f;
     if (lane == 0) scales[r] = scale;
     uint32_t* q4 = reinterpret_cast<uint32_t*>(q + (uint64_t)r * cols);
-    const bool fast = scale_fast_ok(scale);  // wave-uniform
+    const bool fast = scale_fast_ok(scale);  // uniform over the slice
     const float inv = 1.0f / scale;
 #pragma unroll
     for (int it = 0; it < NV; it++) {
-        const uint32_t i = lane + 64 * it;
+        const uint32_t i = lane + T * it;
         if (FULL || i < n4) {
             const float4 t = v[it];
             uint32_t w;
@@ -463,17 +490,18 @@ int rplhip_quantize_per_channel(const float* x, uint32_t num_channels, uint32_t 
     hipStream_t s = as_stream(stream);
     const bool reg = channel_size > 0 && channel_size % 4 == 0 && channel_size <= kRowsWaveMaxCols && (((uintptr_t)x) & 15) == 0 &&
                      (((uintptr_t)q) & 3) == 0;
-    if (reg) {
-        const dim3 grid((num_channels + kThreads / 64 - 1) / (kThreads / 64));
-        const uint32_t nv = (channel_size + 255) / 256;
-#define RPL_QR(NV)                                                                                         \
-    do {                                                                                                   \
-        if (channel_size == 256 * NV)                                                                      \
-            hipLaunchKernelGGL((k_quantize_rows_wave<NV, true>), grid, dim3(kThreads), 0, s, x, num_channels, \
-                               channel_size, q, scales);                                                   \
-        else                                                                                               \
-            hipLaunchKernelGGL((k_quantize_rows_wave<NV, false>), grid, dim3(kThreads), 0, s, x,            \
-                               num_channels, channel_size, q, scales);                                     \
+    if (reg && channel_size >= 1024) {
+        // 4 waves per slice, one slice per block, non-temporal loads
+        const dim3 grid(num_channels);
+        const uint32_t nv = (channel_size + 1023) / 1024;
+#define RPL_QR(NV)                                                                                            \
+    do {                                                                                                      \
+        if (channel_size == 1024 * NV)                                                                        \
+            hipLaunchKernelGGL((k_quantize_rows_wave<NV, 4, true, true>), grid, dim3(kThreads), 0, s, x,       \
+                               num_channels, channel_size, q, scales);                                        \
+        else                                                                                                  \
+            hipLaunchKernelGGL((k_quantize_rows_wave<NV, 4, false, true>), grid, dim3(kThreads), 0, s, x,      \
+                               num_channels, channel_size, q, scales);                                        \
     } while (0)
         if (nv <= 1)
             RPL_QR(1);
@@ -481,12 +509,28 @@ int rplhip_quantize_per_channel(const float* x, uint32_t num_channels, uint32_t 
             RPL_QR(2);
         else if (nv <= 4)
             RPL_QR(4);
-        else if (nv <= 8)
-            RPL_QR(8);
-        else if (nv <= 16)
-            RPL_QR(16);
         else
-            RPL_QR(32);
+            RPL_QR(8);
+#undef RPL_QR
+    } else if (reg) {
+        // shorter slices: one wave each
+        const dim3 grid((num_channels + kThreads / 64 - 1) / (kThreads / 64));
+        const uint32_t nv = (channel_size + 255) / 256;
+#define RPL_QR(NV)                                                                                         \
+    do {                                                                                                   \
+        if (channel_size == 256 * NV)                                                                      \
+            hipLaunchKernelGGL((k_quantize_rows_wave<NV, 1, true, false>), grid, dim3(kThreads), 0, s, x,   \
+                               num_channels, channel_size, q, scales);                                     \
+        else                                                                                               \
+            hipLaunchKernelGGL((k_quantize_rows_wave<NV, 1, false, false>), grid, dim3(kThreads), 0, s, x,  \
+                               num_channels, channel_size, q, scales);                                     \
+    } while (0)
+        if (nv <= 1)
+            RPL_QR(1);
+        else if (nv <= 2)
+            RPL_QR(2);
+        else
+            RPL_QR(4);
 #undef RPL_QR
     } else {
         hipLaunchKernelGGL(k_quantize_rows, dim3(num_channels), dim3(kThreads), 0, s, x, num_channels, channel_size,

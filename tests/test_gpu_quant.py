@@ -158,15 +158,16 @@ def test_quantize_unaligned_pointers(gpu, orc):
 
 
 # Rows of up to 8192 floats with cols % 4 == 0 and aligned rows are held in
-# registers, one wave per row (k_quantize_rows_wave<NV>, 256*NV floats per
-# wave: NV = 1 for 4..256 columns, 2 up to 512, 4 up to 1024, 8 up to 2048,
-# 16 up to 4096, 32 up to 8192; row counts that are not a multiple of the
-# block's 4 rows); others are read twice, one block per row
+# registers (k_quantize_rows_wave<NV, WPR>): rows of 1024 floats or more by 4
+# waves each (NV = 1, 2, 4, 8 float4 per lane for up to 1024, 2048, 4096,
+# 8192 floats; ragged ends re-read the last float4), shorter rows by one wave
+# each (NV = 1, 2, 4 up to 256, 512, 1020; row counts that are not a multiple
+# of the block's 4 rows); others are read twice, one block per row
 # (k_quantize_rows: 33 x 1001, 3 x 9000, odd row starts).
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (8192, 8192), (33, 1001), (3, 9000), (1, 64), (2048, 4096),
                                        (7, 4112), (5, 16), (9, 1004), (6, 8192), (13, 2060), (3, 4),
                                        (11, 260), (6, 512), (10, 1024), (5, 1500), (3, 2048), (2, 3000),
-                                       (17, 252)])
+                                       (17, 252), (5, 1020), (3, 1028), (5, 4100), (4, 7000), (2, 5120)])
 def test_per_channel_vs_oracle(gpu, orc, rows, cols):
     x = rpl_amd.fill_normal(rows * cols, seed(94, 7)).reshape(rows, cols)
     say("per-channel", rows, cols)
@@ -175,7 +176,7 @@ def test_per_channel_vs_oracle(gpu, orc, rows, cols):
     assert bits_equal(q, oq.reshape(-1)) and bits_equal(s, os_)
 
 
-@pytest.mark.parametrize("cols", [48, 4096, 6164])
+@pytest.mark.parametrize("cols", [48, 1024, 2052, 4096, 6164])
 def test_per_channel_special_rows(gpu, orc, cols):
     """Rows that are all zero (scale 0: 0/0 -> -128), hold NaN (never the
     min or max; NaN / scale -> -128), +-inf (scale inf), signed zeros, exact
