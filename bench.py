@@ -424,7 +424,7 @@ def main():
     ms_i8 = wall_i8 = tops = ms_f32 = wall_f32 = tflops = float("nan")
     if want("int8"):
         # At 8192^3 gemm_int8 is exactly one kernel launch
-        # (k_gemm_i8_pairs<kRequantUnit, BKN, no split>, B [K,N] read in place), so
+        # (k_gemm_i8_pairs<kRequantUnit, BKN>, B [K,N] read in place), so
         # these HIP events on its stream time that kernel alone.
         log("bench: int8 gemm_int8 8192^3")
         ms_i8, wall_i8 = timer.time(int8_step, args.steps, args.warmup)
@@ -435,7 +435,7 @@ def main():
         log("bench: int8 NT kernel (linear_int8)")
         ms_nt, _ = timer.time(lambda: check(lib.rplhip_linear_int8(qA.ptr, qB.ptr, None, dC.ptr, n, n, n, stream)),
                               args.steps, args.warmup)
-        nt = {"kernel": "k_gemm_i8_pairs<0, false, false>", "ms_per_launch": round(ms_nt, 4),
+        nt = {"kernel": "k_gemm_i8_pairs<0, false>", "ms_per_launch": round(ms_nt, 4),
               "achieved": round(ops / (ms_nt * 1e-3) / 1e12, 2), "unit": "TOP/s"}
 
     # ---- FP32 8192^3 NN (tensor_gemm semantics, alpha=1, beta=0)
@@ -532,7 +532,7 @@ def main():
 
     # HBM/MALL bytes per launch of the roofline kernel, from the committed
     # FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel of known size).
-    traffic, traffic_kernel = None, "k_gemm_i8_pairs<4, true, false>"
+    traffic, traffic_kernel = None, "k_gemm_i8_pairs<4, true>"
     tpath = os.path.join(REPO, "profiles", "traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:

@@ -496,15 +496,10 @@ __device__ __forceinline__ void epilogue_tile_full(const EpiParams& p, const v16
 // ------------------------------------ NT core GEMM, direct-to-LDS pipeline
 
 
-// Tuning knobs (defaults measured best on MI355X): LDS stages in the ring
-// and where the copies of a tile are issued (0: both operands in the first
-// half of an iteration, 1: both in the second half, 2: A in the first, B in
-// the second).
+// Tuning knob (default measured best on MI355X): LDS stages in the ring.
+// (6 stages for the 256 x 128 tile, which fit, measured the same as 4.)
 #ifndef RPL_I8_STAGES
 #define RPL_I8_STAGES 4
-#endif
-#ifndef RPL_I8_DMA_SLOT
-#define RPL_I8_DMA_SLOT 2
 #endif
 
 namespace dma {
@@ -524,24 +519,43 @@ typedef __attribute__((address_space(3))) v2i* lds_v2i;
 // read depends on are waited for explicitly (vmcnt + barrier), as for the
 // A fragments.
 __device__ __forceinline__ v2i tr8(lds_v2i __restrict__ p) { return __builtin_amdgcn_ds_read_tr8_b64_v2i32(p); }
-constexpr int kSlot = RPL_I8_DMA_SLOT;
 // B-tile height BN = 256 (the big tile) or 128 (grids with too few 256 x
 // 256 tiles to fill the chip): 4 waves (2 x 2), wave tile 128 x BN/2.
 template <int BN>
 struct Geo {
     static_assert(BN == 256 || BN == 128, "B tile of 256 or 128 rows");
-    static_assert(S >= 3 && S * (BM + BN) * BK <= 160 * 1024, "LDS ring must fit 160 KB");
+    static constexpr int kStages = S;
+    static_assert(kStages >= 3 && kStages * (BM + BN) * BK <= 160 * 1024, "LDS ring must fit 160 KB");
     static constexpr int FN = BN / 64;                    // 32-wide MFMA blocks per wave (N side)
     static constexpr int kTileBytesA = BM * BK;           // A part of one stage: 16 KB
     static constexpr int kStageBytes = (BM + BN) * BK;
     static constexpr int kLoadsA = BM / 64, kLoadsB = BN / 64;  // 1 KB copies per wave per tile
     static constexpr int kVmPerTile = kLoadsA + kLoadsB;  // copy instructions per wave per tile
 };
-// Fragments of one 32-k step: 4 A blocks, FN B blocks.
+// Fragments of one 32-k half: 4 A blocks and either FN B blocks (B [N,K])
+// or the two 8-byte transposed halves of each B block (BKN).
+template <bool BKN, int FN>
+struct HalfFrags;
 template <int FN>
-struct Frags {
+struct HalfFrags<false, FN> {
     v4i a[4], b[FN];
+    __device__ v4i bv(int j) const { return b[j]; }
 };
+template <int FN>
+struct HalfFrags<true, FN> {
+    v4i a[4];
+    v2i bl[FN], bh[FN];
+    __device__ v4i bv(int j) const { return (v4i){bl[j].x, bl[j].y, bh[j].x, bh[j].y}; }
+};
+// Fragment reads of a half, in the order its MFMAs (A block m / FN, B block
+// m % FN) first use them: A block 0, the B reads, A blocks 1..3.  Read r < 4
+// is A block r; then B block r - 4 (B [N,K]) or the low / high half of B
+// block (r - 4) / 2 (BKN).
+template <bool BKN, int FN>
+__device__ constexpr int read_at(int m) {
+    constexpr int nb = (BKN ? 2 : 1) * FN;
+    return m == 0 ? 0 : m <= nb ? 3 + m : m - nb;
+}
 }  // namespace dma
 
 // Same tiles, MFMA and fused epilogues as k_gemm_i8_nt<CfgBig>, with the
@@ -584,9 +598,8 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
                                                            uint32_t N, uint32_t K, EpiParams p) {
     using dma::BK;
     using dma::BM;
-    using dma::kSlot;
-    using dma::S;
     using G = dma::Geo<BN>;
+    constexpr int S = G::kStages;
     constexpr int FN = G::FN, kLoadsA = G::kLoadsA, kLoadsB = G::kLoadsB, kVmPerTile = G::kVmPerTile;
     constexpr int kTileBytesA = G::kTileBytesA, kStageBytes = G::kStageBytes;
     static_assert(!BKN || BN == 256, "[K][N] B needs 256-column tiles");
@@ -678,25 +691,27 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
         for (int j = 0; j < 4; j++)
             boff[j] = kTileBytesA + (16 * (g / 2) + e) * 256 + ((8 * wn + 2 * j + g % 2) ^ dma::kn_swz(e)) * 16 + 8 * h;
     }
-    using F = dma::Frags<FN>;
+    using F = dma::HalfFrags<BKN, FN>;
     using dma::lds_v2i;
-    auto fload = [&](uint32_t stage, int kk, F& f) {
-        const int8_t* st = smem + stage * kStageBytes + foff[kk];
-#pragma unroll
-        for (int i = 0; i < 4; i++) f.a[i] = *reinterpret_cast<const v4i*>(st + a_base + i * 32 * BK);
-        if constexpr (BKN) {
-            const int8_t* sb = smem + stage * kStageBytes + kk * 32 * 256;
-#pragma unroll
-            for (int j = 0; j < FN; j++) {
-                const int8_t* pb = sb + boff[j];
-                const v2i lo = dma::tr8((lds_v2i)pb);
-                const v2i hi = dma::tr8((lds_v2i)(pb + 8 * 256));
-                f.b[j] = (v4i){lo.x, lo.y, hi.x, hi.y};
-            }
+    constexpr int kReads = 4 + (BKN ? 2 : 1) * FN;  // fragment reads per half
+    // Read r of stage `stage`, k-half kk (r as in dma::read_at).
+    auto read_one = [&](uint32_t stage, int kk, int r, F& f) {
+        const int8_t* st = smem + stage * kStageBytes;
+        if (r < 4) {
+            f.a[r] = *reinterpret_cast<const v4i*>(st + foff[kk] + a_base + r * 32 * BK);
+        } else if constexpr (BKN) {
+            const int j = (r - 4) / 2, hi = (r - 4) % 2;
+            const v2i t = dma::tr8((lds_v2i)(st + kk * 32 * 256 + boff[j] + hi * 8 * 256));
+            if (hi)
+                f.bh[j] = t;
+            else
+                f.bl[j] = t;
         } else {
-#pragma unroll
-            for (int j = 0; j < FN; j++) f.b[j] = *reinterpret_cast<const v4i*>(st + b_base + j * 32 * BK);
+            f.b[r - 4] = *reinterpret_cast<const v4i*>(st + foff[kk] + b_base + (r - 4) * 32 * BK);
         }
+    };
+    auto fload = [&](uint32_t stage, int kk, F& f) {
+        static_for<kReads>([&](auto R) { read_one(stage, kk, decltype(R)::value, f); });
     };
     v16i acc[4][4];
 #pragma unroll
@@ -708,33 +723,51 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
         for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int j = 0; j < FN; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.bv(j), acc[i][j], 0, 0, 0);
     };
-    // Pin one half's order: fragment reads one per MFMA early, then the
-    // copies of that half (BN = 128 has 8 MFMAs for 6 reads and up to 4
-    // copies: the last two MFMAs take two copies each).
-    auto pin = [&](auto copies_c) {
-        constexpr int copies = decltype(copies_c)::value;
-        if constexpr (FN == 4 && !BKN) {
-            static_for<8>([&](auto) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-            });
-            static_for<copies>([&](auto) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // HBM -> LDS copy
-            });
+    // Copy c of tile kt's copies (A copies first, then B) into `stage`.
+    auto copy_one = [&](uint32_t kt, uint32_t stage, int c) {
+        int8_t* st = smem + stage * kStageBytes;
+        if (c < kLoadsA) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr)(st + (wave * (BM / 4) + c * 16) * BK), 16,
+                                                     voff_a[c], kt * BK, 0, 0);
         } else {
-            constexpr int reads = 4 + (BKN ? 2 : 1) * FN, rest = 4 * FN - reads;
-            static_for<reads>([&](auto) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            });
-            static_for<rest>([&](auto) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x020, (copies + rest - 1) / rest, 0);
-            });
+            const int i = c - kLoadsA;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsrc_b, (lds_ptr)(st + kTileBytesA + (wave * (BN / 4) + i * 16) * BK), 16, voff_b[BKN ? i % 2 : i],
+                BKN ? (kt * BK + 8 * (i / 2)) * ldb : kt * BK, 0, 0);
         }
+    };
+    // Copies of a tile issued in the first half of an iteration (the rest in
+    // the second): with the half's fragment reads, at most one memory
+    // instruction more than MFMAs in either half.
+    constexpr int kCopiesFirst = (kVmPerTile + 1) / 2;
+    // One half: its 4*FN MFMAs on `cur`, each followed by the next memory
+    // instruction of the half -- the kReads fragment reads of `nxt`, then
+    // copies c0 .. c0 + NC - 1 of tile kt_copy -- with a scheduling barrier
+    // after each (left alone, the scheduler bunches the reads just before
+    // their first use and the copies together, and the wave stalls in front
+    // of its next MFMA).  When the half has more memory instructions than
+    // MFMAs, its last MFMAs take two each.
+    auto half = [&](const F& cur, F& nxt, uint32_t rstage, int kk, uint32_t kt_copy, uint32_t cstage, auto C0,
+                    auto NC) {
+        constexpr int c0 = decltype(C0)::value, nc = decltype(NC)::value, nm = 4 * FN;
+        constexpr int ops = kReads + nc, two = ops > nm ? ops - nm : 0;
+        static_for<nm>([&](auto Mc) {
+            constexpr int m = decltype(Mc)::value;
+            acc[m / FN][m % FN] =
+                __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[m / FN], cur.bv(m % FN), acc[m / FN][m % FN], 0, 0, 0);
+            constexpr int first = m < nm - two ? m : (nm - two) + 2 * (m - (nm - two));
+            constexpr int count = m < nm - two ? 1 : 2;
+            static_for<count>([&](auto Oc) {
+                constexpr int o = first + decltype(Oc)::value;
+                if constexpr (o < kReads)
+                    read_one(rstage, kk, dma::read_at<BKN, FN>(o), nxt);
+                else if constexpr (o < ops)
+                    copy_one(kt_copy, cstage, c0 + o - kReads);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
     };
 
     const uint32_t nk = K / BK;
@@ -748,39 +781,25 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
     F f0, f1;
     fload(0, 0, f0);
 
-    // Iteration kt: request tile kt+S-1 (into the stage tile kt-1 left),
-    // read tile kt's second half while multiplying its first, wait for
-    // tile kt+1 and barrier, read tile kt+1's first half while multiplying
-    // kt's second.
-    //
-    // The steady state pins the instruction order (sched_group_barrier):
-    // each fragment read is issued between two MFMAs early in the half, the
-    // tile copies between the later MFMAs, so the MFMA pipe never waits on
-    // an LDS read issued just before it (left alone, the scheduler sinks
-    // every read to just before its first use and reuses its registers).
-    constexpr int kCopiesA = kSlot == 0 ? kVmPerTile : kSlot == 2 ? kLoadsA : 0;
-    constexpr int kCopiesB = kVmPerTile - kCopiesA;
+    // Iteration kt: request tile kt+S-1 (into the stage tile kt-1 left, free
+    // since the barrier of iteration kt-1), read tile kt's second half while
+    // multiplying its first, wait for tile kt+1 and barrier, read tile kt+1's
+    // first half while multiplying kt's second.
     // Copies issued after tile kt+1's at the barrier of iteration kt.
-    constexpr int kLaterSteady = (S - 3) * kVmPerTile + kCopiesA;
+    constexpr int kLaterSteady = (S - 3) * kVmPerTile + kCopiesFirst;
     uint32_t kt = 0;
     for (; kt + 2 * S - 1 <= nk; kt += S) {
         static_for<S>([&](auto U) {
             constexpr int u = decltype(U)::value;
+            const uint32_t tc = kt + u + S - 1, sc = (u + S - 1) % S;
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (kSlot != 1) issue_a(kt + u + S - 1, (u + S - 1) % S);
-            if constexpr (kSlot == 0) issue_b(kt + u + S - 1, (u + S - 1) % S);
-            fload(u, 1, f1);
-            mma(f0);
-            pin(std::integral_constant<int, kCopiesA>{});
-            __builtin_amdgcn_sched_barrier(0);
+            half(f0, f1, u, 1, tc, sc, std::integral_constant<int, 0>{},
+                 std::integral_constant<int, kCopiesFirst>{});
             __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLaterSteady, 0));
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (kSlot == 1) issue_a(kt + u + S - 1, (u + S - 1) % S);
-            if constexpr (kSlot != 0) issue_b(kt + u + S - 1, (u + S - 1) % S);
-            fload((u + 1) % S, 0, f0);
-            mma(f1);
-            pin(std::integral_constant<int, kCopiesB>{});
+            half(f1, f0, (u + 1) % S, 0, tc, sc, std::integral_constant<int, kCopiesFirst>{},
+                 std::integral_constant<int, kVmPerTile - kCopiesFirst>{});
             __builtin_amdgcn_sched_barrier(0);
         });
     }
@@ -839,65 +858,16 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
 // uses, so the wait counts hold to the end and every access stays inside
 // the operands.  Requires K % 128 == 0 and the conditions of
 // k_gemm_i8_nt_dma.
-//
-// SPLIT (stream-K): the grid has one block per CU and block v (in an order
-// that gives each XCD a contiguous range) runs k-steps [v*L, (v+1)*L) of the
-// tiles' concatenated k-steps (tile t owns [t*nkt, (t+1)*nkt)), highest tile
-// first.  A tile whose k-steps span several blocks is finished by the block
-// holding its last k-step (the owner, which reaches it last); the others
-// (producers, which reach it first) store their int32 partial sums with
-// agent-coherent stores (sc1, what agent-scope atomics use; no L2 writeback
-// or invalidate), wait for them, and set their flag to this launch's epoch.
-// The owner polls each producer's flag (bounded: past kSplitSpinCycles it
-// computes that producer's k-steps itself, so the kernel finishes whatever
-// the scheduling), adds the partials (int32 sums are exact in any order)
-// and runs the epilogue.  Producers never wait, and owners wait only for
-// blocks earlier in the same range order.
+
 namespace dma {
 constexpr int kPairBytes = BM * 2 * BK;  // 256 rows x 128 k-bytes
 constexpr int kPairLoads = 8;            // 1 KB copies per wave per A pair
 }  // namespace dma
 
-struct SplitArgs {
-    uint32_t per_block;  // L: k-steps per block (even)
-    uint32_t epoch;      // flag value of this launch (never 0)
-    uint32_t* flags;     // [grid]
-    int32_t* partials;   // [grid][4 waves][64 KiB]
-};
-constexpr uint64_t kSplitSpinCycles = uint64_t(1) << 24;
-constexpr uint32_t kPartialWaveInts = 16384;  // 128 x 128 int32 per wave
-
-// Fragments of one 32-k half: A blocks and either B blocks (B [N,K]) or the
-// two 8-byte transposed halves of each B block (BKN).
-template <bool BKN>
-struct PairFrags;
-template <>
-struct PairFrags<false> {
-    v4i a[4], b[4];
-    __device__ v4i bv(int j) const { return b[j]; }
-};
-template <>
-struct PairFrags<true> {
-    v4i a[4];
-    v2i bl[4], bh[4];
-    __device__ v4i bv(int j) const { return (v4i){bl[j].x, bl[j].y, bh[j].x, bh[j].y}; }
-};
-
-// Tile index (already in XCD-contiguous order) -> tile row / column: groups
-// of kGroupM tile rows walked column by column (as rplhip::tile_of).
-__device__ __forceinline__ void tile_rc(uint32_t t, uint32_t tm, uint32_t tn, uint32_t& im, uint32_t& in) {
-    const uint32_t group = rplhip::kGroupM * tn;
-    const uint32_t g = t / group, first = g * rplhip::kGroupM;
-    const uint32_t gm = tm - first < rplhip::kGroupM ? tm - first : rplhip::kGroupM;
-    const uint32_t w = t - g * group;
-    im = first + w % gm;
-    in = w / gm;
-}
-
-template <int EPI, bool BKN, bool SPLIT>
+template <int EPI, bool BKN>
 __global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restrict__ A, uint32_t lda,
                                                           const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
-                                                          uint32_t N, uint32_t K, EpiParams p, SplitArgs sa) {
+                                                          uint32_t N, uint32_t K, EpiParams p) {
     using dma::BK;
     using dma::BM;
     using dma::kPairBytes;
@@ -905,7 +875,6 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restri
     constexpr int kBStage = BN * BK, kBBase = 2 * kPairBytes;
     constexpr int kReads = BKN ? 12 : 8;  // fragment reads per half
     __shared__ __attribute__((aligned(1024))) int8_t smem[kBBase + S * kBStage];
-    __shared__ uint32_t s_ready;  // SPLIT: a producer's flag as the owner's wave 0 saw it
 
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
@@ -924,7 +893,7 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restri
         for (int j = 0; j < 4; j++)
             boff[j] = (16 * (g / 2) + e) * 256 + ((8 * wn + 2 * j + g % 2) ^ dma::kn_swz(e)) * 16 + 8 * h;
     }
-    using F = PairFrags<BKN>;
+    using F = dma::HalfFrags<BKN, 4>;
     using dma::lds_v2i;
     v16i acc[4][4];
 
@@ -991,17 +960,6 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restri
                                                             (r - 4) * 32 * BK);
             }
         };
-        // Order of the next half's reads: A block 0, the B blocks, A blocks
-        // 1..3 -- the order in which its MFMAs first use them.
-        auto read_at = [](int m) {
-            if constexpr (BKN) {
-                constexpr int o[12] = {0, 4, 5, 6, 7, 8, 9, 10, 11, 1, 2, 3};
-                return o[m];
-            } else {
-                constexpr int o[8] = {0, 4, 5, 6, 7, 1, 2, 3};
-                return o[m];
-            }
-        };
         // One half: MFMA m on `cur`, then read m of `nxt` (m < kReads) or
         // copy m - kReads (the half's 4 copies).
         auto half = [&](const F& cur, F& nxt, uint32_t aslot, uint32_t par, uint32_t stage, int kk, auto copy) {
@@ -1010,7 +968,7 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restri
                 acc[m / 4][m % 4] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[m / 4], cur.bv(m % 4),
                                                                          acc[m / 4][m % 4], 0, 0, 0);
                 if constexpr (m < kReads)
-                    read_one(aslot, par, stage, kk, read_at(m), nxt);
+                    read_one(aslot, par, stage, kk, dma::read_at<BKN, 4>(m), nxt);
                 else if constexpr (m < kReads + 4)
                     copy(m - kReads);
                 __builtin_amdgcn_sched_barrier(0);
@@ -1061,104 +1019,18 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restri
         __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
         __builtin_amdgcn_s_barrier();
     };
-    auto zero_acc = [&] {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int j = 0; j < FN; j++) acc[i][j] = (v16i){};
-    };
-    auto epilogue = [&](uint32_t m0, uint32_t n0) {
-        if (m0 + BM <= M && n0 + BN <= N && p.ldc <= kFullEpiMaxLdc)
-            epilogue_tile_full<EPI, 4, FN, 4>(p, acc, m0 + wm * 128, n0 + wn * (BN / 2), lane);
-        else
-            epilogue_tile<EPI, 4, FN, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * (BN / 2) + lane % 32,
-                                         M, N);
-    };
-
-    if constexpr (!SPLIT) {
-        uint32_t im, in;
-        tile_of(blockIdx.x, tm, tn, im, in);
-        zero_acc();
-        mainloop(im * BM, in * BN, 0, nkt);
-        epilogue(im * BM, in * BN);
-    } else {
-        // Range order: the XCDs (block b runs on XCD b % 8) take contiguous
-        // ranges of blocks, so neighbouring tiles share an XCD's L2.
-        const uint32_t G = gridDim.x, x = blockIdx.x % rplhip::kXcds, q = G / rplhip::kXcds,
-                       r = G % rplhip::kXcds;
-        const uint32_t v = x * q + (x < r ? x : r) + blockIdx.x / rplhip::kXcds;
-        const uint64_t L = sa.per_block, total = (uint64_t)tm * tn * nkt;
-        const uint64_t s0 = (uint64_t)v * L;
-        uint64_t e = s0 + L < total ? s0 + L : total;
-        // A block's partial (at most one: the first segment it runs) lives
-        // in slot v: 4 waves x 64 KiB, lane-interleaved 16-byte pieces.
-        auto slot_rsrc = [&](uint32_t blk) {
-            return uniform_rsrc(sa.partials + ((uint64_t)blk * 4 + wave) * kPartialWaveInts, kPartialWaveInts * 4);
-        };
-        while (e > s0) {
-            const uint32_t t = (uint32_t)((e - 1) / nkt);
-            const uint64_t ts = (uint64_t)t * nkt;
-            const uint64_t sb = s0 > ts ? s0 : ts;
-            const uint32_t k0 = (uint32_t)(sb - ts), k1 = (uint32_t)(e - ts);
-            uint32_t im, in;
-            tile_rc(t, tm, tn, im, in);
-            zero_acc();
-            mainloop(im * BM, in * BN, k0, k1 - k0);
-            if (k0 == 0 && k1 == nkt) {
-                epilogue(im * BM, in * BN);
-            } else if (k1 < nkt) {
-                // Producer: publish the partial sums, then the flag.
-                const __amdgpu_buffer_rsrc_t rs = slot_rsrc(v);
-                static_for<64>([&](auto I) {
-                    constexpr int idx = decltype(I)::value;
-                    constexpr int i = idx / 16, j = (idx / 4) % 4, r4 = idx % 4;
-                    const v4i w = (v4i){acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2],
-                                        acc[i][j][4 * r4 + 3]};
-                    __builtin_amdgcn_raw_buffer_store_b128(w, rs, lane * 16, idx * 1024, 16 /* sc1 */);
-                });
-                __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
-                __builtin_amdgcn_s_barrier();
-                if (threadIdx.x == 0) __hip_atomic_store(sa.flags + v, sa.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            } else {
-                // Owner: the producers are the blocks from ts / L to v - 1.
-                const uint32_t first = (uint32_t)(ts / L);
-                for (uint32_t pb = first; pb < v; pb++) {
-                    if (threadIdx.x == 0) {
-                        const uint64_t t_start = __builtin_amdgcn_s_memtime();
-                        uint32_t ok = 0;
-                        while (!(ok = __hip_atomic_load(sa.flags + pb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                                      sa.epoch) &&
-                               __builtin_amdgcn_s_memtime() - t_start < kSplitSpinCycles)
-                            __builtin_amdgcn_s_sleep(2);
-                        s_ready = ok;
-                    }
-                    __syncthreads();
-                    const uint32_t ready = __builtin_amdgcn_readfirstlane(s_ready);
-                    __syncthreads();
-                    if (ready) {
-                        const __amdgpu_buffer_rsrc_t rs = slot_rsrc(pb);
-                        static_for<64>([&](auto I) {
-                            constexpr int idx = decltype(I)::value;
-                            constexpr int i = idx / 16, j = (idx / 4) % 4, r4 = idx % 4;
-                            const v4i w = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, idx * 1024, 16 /* sc1 */);
-                            acc[i][j][4 * r4] = wrap_add(acc[i][j][4 * r4], w.x);
-                            acc[i][j][4 * r4 + 1] = wrap_add(acc[i][j][4 * r4 + 1], w.y);
-                            acc[i][j][4 * r4 + 2] = wrap_add(acc[i][j][4 * r4 + 2], w.z);
-                            acc[i][j][4 * r4 + 3] = wrap_add(acc[i][j][4 * r4 + 3], w.w);
-                        });
-                    } else {
-                        // Not published in time: compute producer pb's
-                        // k-steps of this tile here instead.
-                        const uint64_t ps = (uint64_t)pb * L > ts ? (uint64_t)pb * L : ts;
-                        const uint64_t pe = ((uint64_t)pb + 1) * L < ts + nkt ? ((uint64_t)pb + 1) * L : ts + nkt;
-                        mainloop(im * BM, in * BN, (uint32_t)(ps - ts), (uint32_t)(pe - ps));
-                    }
-                }
-                epilogue(im * BM, in * BN);
-            }
-            e = sb;
-        }
-    }
+        for (int j = 0; j < FN; j++) acc[i][j] = (v16i){};
+    uint32_t im, in;
+    tile_of(blockIdx.x, tm, tn, im, in);
+    const uint32_t m0 = im * BM, n0 = in * BN;
+    mainloop(m0, n0, 0, nkt);
+    if (m0 + BM <= M && n0 + BN <= N && p.ldc <= kFullEpiMaxLdc)
+        epilogue_tile_full<EPI, 4, FN, 4>(p, acc, m0 + wm * 128, n0 + wn * (BN / 2), lane);
+    else
+        epilogue_tile<EPI, 4, FN, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * (BN / 2) + lane % 32, M, N);
 }
 
 // --------------------------------------------------- skinny (M <= 16) GEMM
@@ -1761,8 +1633,8 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
             const EpiParams p2 = shift_cols(p, n1);
             const uint32_t tiles1 = (uint32_t)(mt * (n1 / 256)), tiles2 = (uint32_t)(mt * ((N - n1 + 127) / 128));
             if (use_pairs(K))
-                hipLaunchKernelGGL((k_gemm_i8_pairs<EPI, false, false>), dim3(tiles1), dim3(dma::kThreads), 0, s, A, lda,
-                                   B, ldb, M, n1, K, p, SplitArgs{});
+                hipLaunchKernelGGL((k_gemm_i8_pairs<EPI, false>), dim3(tiles1), dim3(dma::kThreads), 0, s, A, lda,
+                                   B, ldb, M, n1, K, p);
             else
                 hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256>), dim3(tiles1), dim3(dma::kThreads), 0, s, A, lda, B,
                                    ldb, M, n1, K, p);
@@ -1773,8 +1645,8 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
         if (dma_ok) {
             const uint64_t tiles = mt * ((N + 255) / 256);
             if (use_pairs(K))
-                hipLaunchKernelGGL((k_gemm_i8_pairs<EPI, false, false>), dim3((uint32_t)tiles), dim3(dma::kThreads),
-                                   0, s, A, lda, B, ldb, M, N, K, p, SplitArgs{});
+                hipLaunchKernelGGL((k_gemm_i8_pairs<EPI, false>), dim3((uint32_t)tiles), dim3(dma::kThreads),
+                                   0, s, A, lda, B, ldb, M, N, K, p);
             else
                 hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256>), dim3((uint32_t)tiles), dim3(dma::kThreads), 0, s, A,
                                    lda, B, ldb, M, N, K, p);
@@ -1812,8 +1684,8 @@ int launch_kn(const int8_t* A, const int8_t* B, uint32_t M, uint32_t N, uint32_t
               hipStream_t s) {
     const uint32_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
     if (use_pairs(K))
-        hipLaunchKernelGGL((k_gemm_i8_pairs<EPI, true, false>), dim3(tiles), dim3(dma::kThreads), 0, s, A, K, B, N,
-                           M, N, K, p, SplitArgs{});
+        hipLaunchKernelGGL((k_gemm_i8_pairs<EPI, true>), dim3(tiles), dim3(dma::kThreads), 0, s, A, K, B, N,
+                           M, N, K, p);
     else
         hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256, true>), dim3(tiles), dim3(dma::kThreads), 0, s, A, K, B, N, M,
                            N, K, p);
