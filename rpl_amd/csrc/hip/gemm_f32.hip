@@ -934,6 +934,62 @@ __global__ void __launch_bounds__(256) k_sgemm_valu(uint32_t M, uint32_t N, uint
     if (bias) out2[(uint64_t)m * ldc + n] = c + bias[n];  // separately rounded, as src/rpl_core.c:112-120
 }
 
+// The same chain for A as [M,K] and B as [N,K] with few columns (the MLP's
+// 4096 x 10 x 128): the block's 256 outputs need only rows m0..m1 of A and
+// all N rows of B, which it first copies into LDS with 128-bit loads (one
+// round of memory latency instead of one per 32 k), then every thread runs
+// its fma chain from LDS.  Rows are padded to K + 4 floats, so the rows read
+// together fall on distinct banks.
+__global__ void __launch_bounds__(256) k_sgemm_valu_lds(uint32_t M, uint32_t N, uint32_t K, float alpha,
+                                                        const float* __restrict__ A, uint32_t lda,
+                                                        const float* __restrict__ B, uint32_t ldb, float beta,
+                                                        float* __restrict__ C, uint32_t ldc, int read_c,
+                                                        const float* __restrict__ bias, float* __restrict__ out2) {
+    extern __shared__ __attribute__((aligned(16))) float lds_ab[];
+    const uint32_t pitch = K + 4, k4 = K / 4;
+    const uint64_t i0 = (uint64_t)blockIdx.x * 256, total = (uint64_t)M * N;
+    const uint64_t ilast = i0 + 255 < total ? i0 + 255 : total - 1;
+    const uint32_t m0 = (uint32_t)(i0 / N), rows_a = (uint32_t)(ilast / N) - m0 + 1;
+    float* as = lds_ab;
+    float* bs = lds_ab + (uint64_t)rows_a * pitch;
+    for (uint32_t c = threadIdx.x; c < rows_a * k4; c += 256) {
+        const uint32_t r = c / k4, q = c % k4;
+        *reinterpret_cast<float4*>(&as[r * pitch + 4 * q]) =
+            *reinterpret_cast<const float4*>(A + (uint64_t)(m0 + r) * lda + 4 * q);
+    }
+    for (uint32_t c = threadIdx.x; c < N * k4; c += 256) {
+        const uint32_t r = c / k4, q = c % k4;
+        *reinterpret_cast<float4*>(&bs[r * pitch + 4 * q]) =
+            *reinterpret_cast<const float4*>(B + (uint64_t)r * ldb + 4 * q);
+    }
+    __syncthreads();
+    const uint64_t i = i0 + threadIdx.x;
+    if (i >= total) return;
+    const uint32_t m = (uint32_t)(i / N), n = (uint32_t)(i % N);
+    const float4* a4 = reinterpret_cast<const float4*>(&as[(m - m0) * pitch]);
+    const float4* b4 = reinterpret_cast<const float4*>(&bs[n * pitch]);
+    float sum = 0.0f;
+#pragma unroll 8
+    for (uint32_t q = 0; q < k4; q++) {
+        const float4 a = a4[q], b = b4[q];
+        sum = __builtin_fmaf(a.x, b.x, sum);
+        sum = __builtin_fmaf(a.y, b.y, sum);
+        sum = __builtin_fmaf(a.z, b.z, sum);
+        sum = __builtin_fmaf(a.w, b.w, sum);
+    }
+    float* cp = &C[(uint64_t)m * ldc + n];
+    const float c = __builtin_fmaf(alpha, sum, read_c ? beta * *cp : 0.0f);
+    *cp = c;
+    if (bias) out2[(uint64_t)m * ldc + n] = c + bias[n];  // separately rounded, as src/rpl_core.c:112-120
+}
+// LDS the block needs, or 0 when the shape does not suit k_sgemm_valu_lds.
+size_t valu_lds_bytes(uint32_t N, uint32_t K) {
+    if (K == 0 || K % 4 || N > 64) return 0;
+    const size_t rows = 256 / N + 2 + N;
+    const size_t bytes = rows * (K + 4) * sizeof(float);
+    return bytes <= 64 * 1024 ? bytes : 0;
+}
+
 constexpr uint32_t kValuMaxK = 256;
 constexpr uint64_t kValuMaxWork = 1ull << 23;
 
@@ -988,6 +1044,12 @@ int launch(uint32_t M, uint32_t N, uint32_t K, float alpha, const float* A, uint
     if (valu) {
         const uint64_t blocks = ((uint64_t)M * N + 255) / 256;  // M*N <= 2^23
         if constexpr (!TA && TB) {
+            const size_t lds = valu_lds_bytes(N, K);
+            if (lds && aligned16(A) && aligned16(B) && lda % 4 == 0 && ldb % 4 == 0) {
+                hipLaunchKernelGGL(k_sgemm_valu_lds, dim3((uint32_t)blocks), dim3(256), lds, s, M, N, K, alpha, A, lda,
+                                   B, ldb, beta, C, ldc, read_c, bias, out2);
+                return rplhip::check_launch("sgemm (VALU, LDS)");
+            }
             if (aligned16(A) && aligned16(B) && lda % 4 == 0 && ldb % 4 == 0) {
                 hipLaunchKernelGGL((k_sgemm_valu<false, true, true>), dim3((uint32_t)blocks), dim3(256), 0, s, M, N,
                                    K, alpha, A, lda, B, ldb, beta, C, ldc, read_c, bias, out2);

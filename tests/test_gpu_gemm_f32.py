@@ -60,16 +60,19 @@ def test_sgemm_small_vs_oracle(gpu, orc, M, N, K, ta, tb):
             assert gemm_err_ratio(out, op(A, ta), op(B, tb), ref, alpha, beta, C0) <= fp32_tol(K)
 
 
-def test_sgemm_small_padded_rows_bit_exact(gpu, orc):
-    # A as [M,K] and B as [N,K] with 16-byte aligned rows (lda = ldb = 132)
-    # and K % 4 == 2: 128-bit loads for k < 128, then two scalar steps; the
-    # fma chain is the reference's either way.
-    rng = np.random.default_rng(11)
-    M, N, K, ld = 64, 16, 130, 132
+@pytest.mark.parametrize("M,N,K,ld", [(64, 16, 130, 132), (64, 16, 128, 132), (1000, 1, 32, 36), (100, 64, 128, 128),
+                                      (77, 3, 252, 256)])
+def test_sgemm_small_padded_rows_bit_exact(gpu, orc, M, N, K, ld):
+    # A as [M,K] and B as [N,K] with 16-byte aligned rows: K % 4 == 0 and
+    # N <= 64 stage the block's rows in LDS (k_sgemm_valu_lds: N = 1, 16, 64,
+    # ragged last blocks); (77, 3, 252) would need more than 64 KB of LDS and
+    # K % 4 == 2 cannot stage, so both take 128-bit loads from memory (with
+    # two scalar steps for K = 130); the fma chain is the reference's always.
+    rng = np.random.default_rng(M + N + K)
     Abig = rng.uniform(-1, 1, (M, ld)).astype(np.float32)
     Bbig = rng.uniform(-1, 1, (N, ld)).astype(np.float32)
     C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
-    say("sgemm small padded rows")
+    say("sgemm small padded rows", M, N, K, ld)
     out = sgemm(Abig, Bbig, C0, M, N, K, 0.75, -0.5, 0, 1, lda=ld, ldb=ld)
     ref = orc.sgemm(Abig[:, :K].copy(), Bbig[:, :K].copy(), C0, M, N, K, 0.75, -0.5, False, True)
     assert bits_equal(out, ref)
@@ -163,6 +166,30 @@ def test_sgemm_wave_split_vs_float64(gpu, M, N, K, ta, tb):
     ok = ~np.isnan(ref)
     assert gemm_err_ratio(np.where(ok, out, 0), op(A, ta), op(B, tb), np.where(ok, ref, 0), alpha, beta,
                           np.nan_to_num(C0)) <= fp32_tol(K)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_wave_split_leading_dimensions(gpu, ta, tb):
+    # Sub-matrix views on the wave-split kernel: lda / ldb / ldc past the
+    # extents (multiples of 4 floats), padding left untouched.
+    rng = np.random.default_rng(20 + 2 * ta + tb)
+    M, N, K = 64, 96, 1000
+    pa, pb, pc = 12, 8, 4
+    Abig = rng.uniform(-1, 1, (K, M + pa) if ta else (M, K + pa)).astype(np.float32)
+    Bbig = rng.uniform(-1, 1, (N, K + pb) if tb else (K, N + pb)).astype(np.float32)
+    Cbig = rng.uniform(-1, 1, (M, N + pc)).astype(np.float32)
+    Cbig[5, 7] = np.nan
+    lda, ldb, ldc = Abig.shape[1], Bbig.shape[1], N + pc
+    say("sgemm wave split ld", ta, tb)
+    out = sgemm(Abig, Bbig, Cbig, M, N, K, 0.75, -0.5, ta, tb, lda=lda, ldb=ldb, ldc=ldc)
+    A = Abig[:, :M] if ta else Abig[:, :K]
+    B = Bbig[:, :K] if tb else Bbig[:, :N]
+    assert np.array_equal(out[:, N:], Cbig[:, N:])  # untouched padding
+    assert np.isnan(out[5, 7]) and np.isnan(out[:, :N]).sum() == 1
+    ref = 0.75 * (op(A, ta).astype(np.float64) @ op(B, tb).astype(np.float64)) - 0.5 * Cbig[:, :N].astype(np.float64)
+    ok = ~np.isnan(ref)
+    assert gemm_err_ratio(np.where(ok, out[:, :N], 0), op(A, ta), op(B, tb), np.where(ok, ref, 0), 0.75, -0.5,
+                          np.nan_to_num(Cbig[:, :N])) <= fp32_tol(K)
 
 
 def test_sgemm_leading_dimensions(gpu, orc):
