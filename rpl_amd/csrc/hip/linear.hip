@@ -43,19 +43,28 @@ __global__ void __launch_bounds__(kThreads) k_relu(const float* __restrict__ x, 
     }
 }
 
-// rpl_core.c:421.  overwrite: dx holds zeros only logically and is written
-// (0.0f + dy, or 0.0f where x <= 0), the bits of the accumulation into +0.0.
+// rpl_core.c:421: the new value of one element of the input's gradient.
+// overwrite: the gradient holds zeros only logically (0.0f + dy, or 0.0f
+// where x <= 0: the bits of the accumulation into +0.0); else base += dy
+// where x > 0.
+__device__ __forceinline__ float relu_grad_acc(bool overwrite, float base, float x, float dy) {
+    return overwrite ? (x > 0 ? 0.0f + dy : 0.0f) : (x > 0 ? base + dy : base);
+}
 __global__ void __launch_bounds__(kThreads) k_relu_backward(const float* __restrict__ x,
                                                             const float* __restrict__ dy,
                                                             float* __restrict__ dx, uint64_t n, int overwrite) {
     if (overwrite) {
-        GRID_STRIDE(i, n) { dx[i] = x[i] > 0 ? 0.0f + dy[i] : 0.0f; }
+        GRID_STRIDE(i, n) { dx[i] = relu_grad_acc(true, 0.0f, x[i], dy[i]); }
     } else {
         GRID_STRIDE(i, n) {
-            if (x[i] > 0) dx[i] += dy[i];
+            if (x[i] > 0) dx[i] = relu_grad_acc(false, dx[i], x[i], dy[i]);
         }
     }
 }
+
+// rpl_core.c:441-444: one element of the predictions' gradient, base +
+// (g0 * 2/n) * (p - t), which contracts to fma(g0f, p - t, base).
+__device__ __forceinline__ float mse_grad_acc(float base, float g0f, float p, float t) { return base + g0f * (p - t); }
 
 // rpl_core.c:324 (overwrite: dx = 0.0f + dy, as into a zeroed dx)
 __global__ void __launch_bounds__(kThreads) k_accumulate(const float* __restrict__ dy,
@@ -76,17 +85,38 @@ constexpr int kRowLanes = kThreads / kColTile;
 // DX: also pass the gradient through to backward_add's other operand,
 // dx = dx + dy (overwrite: 0.0f + dy), as k_accumulate does; every element
 // of dy is visited exactly once.
-template <bool DX>
+// SRC: where dy comes from.  kSrcGrad: read it.  kSrcRelu / kSrcMse: it is
+// the add output's gradient right after the ReLU / MSE backward that
+// follows the add in the graph accumulated into it (the autograd walk runs
+// backward_add right after that accumulation): the element is computed
+// here as k_relu_backward / k_mse_backward would, written to that gradient,
+// and used as dy (one pass instead of two).
+enum { kSrcGrad = 0, kSrcRelu = 1, kSrcMse = 2 };
+template <bool DX, int SRC>
 __global__ void __launch_bounds__(kThreads) k_colsum_partial(const float* __restrict__ dy, uint64_t n,
                                                              uint64_t rows, uint64_t nb,
                                                              uint64_t rows_per_split,
                                                              float* __restrict__ part, float* __restrict__ dx,
-                                                             int dx_overwrite) {
+                                                             int dx_overwrite, RplGradSrc src) {
     __shared__ float red[kRowLanes][kColTile];
     uint64_t c = (uint64_t)blockIdx.x * kColTile + threadIdx.x % kColTile;
     int lane_r = threadIdx.x / kColTile;
     uint64_t r0 = (uint64_t)blockIdx.y * rows_per_split;
     uint64_t r1 = r0 + rows_per_split < rows ? r0 + rows_per_split : rows;
+    const float g0f = SRC == kSrcMse ? (src.g0p ? *src.g0p : src.g0v) * (2.0f / (float)n) : 0.0f;
+    // dy at element i (SRC != kSrcGrad: also written to the add output's
+    // gradient).
+    auto value = [&](uint64_t i) {
+        if constexpr (SRC == kSrcGrad) {
+            return dy[i];
+        } else {
+            const float base = src.g_overwrite ? 0.0f : src.g[i];
+            const float v = SRC == kSrcRelu ? relu_grad_acc(src.g_overwrite, base, src.x[i], src.y[i])
+                                            : mse_grad_acc(base, g0f, src.x[i], src.y[i]);
+            src.g[i] = v;
+            return v;
+        }
+    };
     // Rows in batches of 4 loads in flight, added in row order (a chain of
     // one load per row was latency-bound: 6-7 us for [4096, 128]).
     float g = 0;
@@ -99,7 +129,7 @@ __global__ void __launch_bounds__(kThreads) k_colsum_partial(const float* __rest
             for (int j = 0; j < 4; j++) {
                 const uint64_t i = (r + j * kRowLanes) * nb + c;
                 ok[j] = i < n;
-                v[j] = ok[j] ? dy[i] : 0.0f;
+                v[j] = ok[j] ? value(i) : 0.0f;
             }
 #pragma unroll
             for (int j = 0; j < 4; j++)
@@ -114,7 +144,7 @@ __global__ void __launch_bounds__(kThreads) k_colsum_partial(const float* __rest
         }
         for (; r < r1; r += kRowLanes)
             if (r * nb + c < n) {
-                const float v = dy[r * nb + c];
+                const float v = value(r * nb + c);
                 g += v;
                 if constexpr (DX) dx[r * nb + c] = (dx_overwrite ? 0.0f : dx[r * nb + c]) + v;
             }
@@ -127,33 +157,32 @@ __global__ void __launch_bounds__(kThreads) k_colsum_partial(const float* __rest
         part[(uint64_t)blockIdx.y * nb + c] = s;
     }
 }
-
-// Stage 2: db[c] += sum over splits (rpl_core.c:333).  Block = 64 columns x
-// 4 row lanes; lane r sums splits r, r+4, ... with 4 independent loads in
-// flight (a chain of one load per split was latency-bound: 11.6 us for 64
-// splits), then the lane sums are added in lane order (deterministic).
+// Stage 2: db[c] (+)= the sum of column c's split partials.  A block takes
+// 16 columns with 16 lanes each; lane l adds partials l, l+16, .. (4 loads in
+// flight), then lane 0 adds the 16 lane sums in lane order.
+constexpr int kFinCols = 16, kFinLanes = kThreads / kFinCols;
 __global__ void __launch_bounds__(kThreads) k_colsum_finish(const float* __restrict__ part, int splits,
                                                             uint64_t nb, float* __restrict__ db, int overwrite) {
-    __shared__ float red[kRowLanes][kColTile];
-    const uint64_t c = (uint64_t)blockIdx.x * kColTile + threadIdx.x % kColTile;
-    const int lane_r = threadIdx.x / kColTile;
+    __shared__ float red[kFinLanes][kFinCols];
+    const uint64_t c = (uint64_t)blockIdx.x * kFinCols + threadIdx.x % kFinCols;
+    const int lane = threadIdx.x / kFinCols;
     float s = 0;
     if (c < nb) {
-        int k = lane_r;
-        for (; k + 3 * kRowLanes < splits; k += 4 * kRowLanes) {
+        int k = lane;
+        for (; k + 3 * kFinLanes < splits; k += 4 * kFinLanes) {
             float v[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = part[(uint64_t)(k + j * kRowLanes) * nb + c];
+            for (int j = 0; j < 4; j++) v[j] = part[(uint64_t)(k + j * kFinLanes) * nb + c];
 #pragma unroll
             for (int j = 0; j < 4; j++) s += v[j];
         }
-        for (; k < splits; k += kRowLanes) s += part[(uint64_t)k * nb + c];
+        for (; k < splits; k += kFinLanes) s += part[(uint64_t)k * nb + c];
     }
-    red[lane_r][threadIdx.x % kColTile] = s;
+    red[lane][threadIdx.x % kFinCols] = s;
     __syncthreads();
-    if (lane_r == 0 && c < nb) {
+    if (lane == 0 && c < nb) {
         float t = red[0][threadIdx.x];
-        for (int r = 1; r < kRowLanes; r++) t += red[r][threadIdx.x];
+        for (int r = 1; r < kFinLanes; r++) t += red[r][threadIdx.x];
         db[c] = (overwrite ? 0.0f : db[c]) + t;
     }
 }
@@ -241,9 +270,9 @@ __global__ void __launch_bounds__(kThreads) k_mse_backward(const float* __restri
                                                            const float* __restrict__ t, uint64_t n,
                                                            const float* __restrict__ g0p, float g0v,
                                                            float* __restrict__ dp, int overwrite) {
-    float factor = 2.0f / (float)n;
-    float g0 = g0p ? *g0p : g0v;
-    GRID_STRIDE(i, n) { dp[i] = (overwrite ? 0.0f : dp[i]) + g0 * factor * (p[i] - t[i]); }
+    const float factor = 2.0f / (float)n;
+    const float g0f = (g0p ? *g0p : g0v) * factor;
+    GRID_STRIDE(i, n) { dp[i] = mse_grad_acc(overwrite ? 0.0f : dp[i], g0f, p[i], t[i]); }
 }
 
 // Activations of the device seam (tensor_sigmoid_gpu / tensor_tanh_gpu /
@@ -424,9 +453,10 @@ ColsumPlan colsum_plan(uint64_t n, uint64_t nb) {
     // backward_add's j-loop visits i, i+nb, ... < n: ceil(n/nb) rows.
     c.full_rows = (n + nb - 1) / nb;
     c.cx = (nb + kColTile - 1) / kColTile;
-    // Enough row splits to put ~4 blocks on every CU, each split >= 64 rows.
+    // Enough row splits to put ~4 blocks on every CU, each split >= 16 rows
+    // (4 rows per thread: one batch of loads).
     uint64_t want = (4ull * cu_count() + c.cx - 1) / c.cx;
-    uint64_t splits = c.full_rows / 64;
+    uint64_t splits = c.full_rows / 16;
     if (splits > want) splits = want;
     if (splits < 1) splits = 1;
     if (splits > 65535) splits = 65535;
@@ -450,31 +480,46 @@ int rplhip__bias_grad(const float* dy, uint64_t n, float* db, uint64_t nb, int o
     if (st) return st;
     // A ragged last row (n % nb != 0, columns < n % nb get one more term) is
     // handled by the r*nb + c < n bound in the partial kernel.
-    hipLaunchKernelGGL(k_colsum_partial<false>, dim3((unsigned)c.cx, (unsigned)c.splits), dim3(kThreads), 0, s, dy,
-                       n, c.full_rows, nb, c.rps, (float*)ws, (float*)nullptr, 0);
-    hipLaunchKernelGGL(k_colsum_finish, dim3((unsigned)c.cx), dim3(kThreads), 0, s, (const float*)ws, (int)c.splits,
+    hipLaunchKernelGGL((k_colsum_partial<false, kSrcGrad>), dim3((unsigned)c.cx, (unsigned)c.splits), dim3(kThreads),
+                       0, s, dy, n, c.full_rows, nb, c.rps, (float*)ws, (float*)nullptr, 0, RplGradSrc{});
+    hipLaunchKernelGGL(k_colsum_finish, dim3((unsigned)((nb + kFinCols - 1) / kFinCols)), dim3(kThreads), 0, s,
+                       (const float*)ws, (int)c.splits,
                        nb, db, overwrite);
     st = check_launch("bias_grad");
     ws_free(ws, s);
     return st;
 }
 
-int rplhip__add_backward_begin(const float* dy, uint64_t n, float* dx, int dx_overwrite, uint64_t nb, RplColsum* cs,
-                               rplhip_stream_t stream) {
+int rplhip__add_backward_begin(const float* dy, uint64_t n, float* dx, int dx_overwrite, uint64_t nb,
+                               const RplGradSrc* src, RplColsum* cs, rplhip_stream_t stream) {
     cs->ws = nullptr;
     cs->splits = 0;
     cs->nb = nb;
     if (n == 0) return RPLHIP_OK;
-    NEED(dy && dx, "rplhip_add_backward");
-    if (nb == 0) return rplhip__accumulate(dy, dx, n, dx_overwrite, stream);
+    const int kind = src ? src->kind : kSrcGrad;
+    NEED(dx && (kind == kSrcGrad ? dy != nullptr : src->x && src->y && src->g), "rplhip_add_backward");
+    NEED(kind == kSrcGrad || kind == kSrcRelu || kind == kSrcMse, "rplhip_add_backward (source)");
+    if (nb == 0) {
+        NEED(kind == kSrcGrad, "rplhip_add_backward (fused source without a bias)");
+        return rplhip__accumulate(dy, dx, n, dx_overwrite, stream);
+    }
     RPLHIP_REQUIRE_DEVICE();
     hipStream_t s = as_stream(stream);
     const ColsumPlan c = colsum_plan(n, nb);
     int st = ws_alloc(&cs->ws, sizeof(float) * c.splits * nb, s);
     if (st) return st;
     cs->splits = c.splits;
-    hipLaunchKernelGGL(k_colsum_partial<true>, dim3((unsigned)c.cx, (unsigned)c.splits), dim3(kThreads), 0, s, dy,
-                       n, c.full_rows, nb, c.rps, (float*)cs->ws, dx, dx_overwrite);
+    const dim3 grid((unsigned)c.cx, (unsigned)c.splits);
+    const RplGradSrc sv = src ? *src : RplGradSrc{};
+    if (kind == kSrcRelu)
+        hipLaunchKernelGGL((k_colsum_partial<true, kSrcRelu>), grid, dim3(kThreads), 0, s, dy, n, c.full_rows, nb,
+                           c.rps, (float*)cs->ws, dx, dx_overwrite, sv);
+    else if (kind == kSrcMse)
+        hipLaunchKernelGGL((k_colsum_partial<true, kSrcMse>), grid, dim3(kThreads), 0, s, dy, n, c.full_rows, nb,
+                           c.rps, (float*)cs->ws, dx, dx_overwrite, sv);
+    else
+        hipLaunchKernelGGL((k_colsum_partial<true, kSrcGrad>), grid, dim3(kThreads), 0, s, dy, n, c.full_rows, nb,
+                           c.rps, (float*)cs->ws, dx, dx_overwrite, sv);
     st = check_launch("add_backward");
     if (st) {
         ws_free(cs->ws, s);
@@ -488,7 +533,7 @@ int rplhip__add_backward_finish(RplColsum* cs, float* db, int db_overwrite, rplh
     hipStream_t s = as_stream(stream);
     int st = RPLHIP_OK;
     if (db) {
-        hipLaunchKernelGGL(k_colsum_finish, dim3((unsigned)((cs->nb + kColTile - 1) / kColTile)), dim3(kThreads), 0,
+        hipLaunchKernelGGL(k_colsum_finish, dim3((unsigned)((cs->nb + kFinCols - 1) / kFinCols)), dim3(kThreads), 0,
                            s, (const float*)cs->ws, (int)cs->splits, cs->nb, db, db_overwrite);
         st = check_launch("add_backward (bias)");
     }

@@ -146,28 +146,42 @@ Tensor* tensor_mse_loss(const Tensor* pred, const Tensor* target) {
 
 /* src/rpl_core.c:319-337.  Gradients are accumulated; a device gradient
  * that is still zero only logically is overwritten instead (the same bits). */
+/* backward_add's path with t, both parents and their gradients on the
+ * device: one pass over dy writes a's gradient and the bias gradient's
+ * column partial sums, which are added into b's gradient after a's
+ * subgraph, in the reference's order.  src (may be NULL): dy is t's
+ * gradient right after the ReLU / MSE backward that consumes t
+ * accumulated into it, computed within the same pass (see RplGradSrc). */
+static int add_backward_device_ok(const Tensor* t) {
+    const Tensor* a = t->parent1;
+    const Tensor* b = t->parent2;
+    return t->backward_fn == backward_add && t->grad && a && a->grad && b && b->grad && b->size > 0 &&
+           rpl__is_gpu(t) && rpl__is_gpu(a) && rpl__is_gpu(b);
+}
+static void add_backward_device(Tensor* t, const RplGradSrc* src) {
+    Tensor* a = t->parent1;
+    Tensor* b = t->parent2;
+    RplStage s = {0};
+    int ow_a = 0, ow_b = 0;
+    RplColsum cs = {0};
+    const float* dy = src ? NULL : rpl__view_grad(&s, t, 1, 0);
+    float* da = rpl__view_grad_acc(&s, a, &ow_a);
+    if (!s.err)
+        s.err = !rpl__ok(rplhip__add_backward_begin(dy, t->size, da, ow_a, b->size, src, &cs, NULL), "backward_add");
+    rpl__stage_finish(&s);
+    if (a->backward_fn) a->backward_fn(a);
+    RplStage s2 = {0};
+    float* db = s.err ? NULL : rpl__view_grad_acc(&s2, b, &ow_b);
+    if (!rpl__ok(rplhip__add_backward_finish(&cs, s2.err ? NULL : db, ow_b, NULL), "backward_add (bias)")) s2.err = 1;
+    rpl__stage_finish(&s2);
+    if (b->backward_fn) b->backward_fn(b);
+}
+
 void backward_add(Tensor* t) {
     Tensor* a = t->parent1;
     Tensor* b = t->parent2;
     if (a && a->grad && b && b->grad && rpl__is_gpu(t) && rpl__is_gpu(a) && rpl__is_gpu(b)) {
-        /* All on the device: one pass over dy writes a's gradient and the
-         * bias gradient's column partial sums, which are added into b's
-         * gradient after a's subgraph, in the reference's order. */
-        RplStage s = {0};
-        int ow_a = 0, ow_b = 0;
-        RplColsum cs = {0};
-        const float* dy = rpl__view_grad(&s, t, 1, 0);
-        float* da = rpl__view_grad_acc(&s, a, &ow_a);
-        if (!s.err)
-            s.err = !rpl__ok(rplhip__add_backward_begin(dy, t->size, da, ow_a, b->size, &cs, NULL), "backward_add");
-        rpl__stage_finish(&s);
-        if (a->backward_fn) a->backward_fn(a);
-        RplStage s2 = {0};
-        float* db = s.err ? NULL : rpl__view_grad_acc(&s2, b, &ow_b);
-        if (!rpl__ok(rplhip__add_backward_finish(&cs, s2.err ? NULL : db, ow_b, NULL), "backward_add (bias)"))
-            s2.err = 1;
-        rpl__stage_finish(&s2);
-        if (b->backward_fn) b->backward_fn(b);
+        add_backward_device(t, NULL);
         return;
     }
     if (a && a->grad) {
@@ -240,6 +254,18 @@ void backward_matmul(Tensor* t) {
 /* src/rpl_core.c:418-424 */
 void backward_relu(Tensor* t) {
     Tensor* a = t->parent1;
+    if (a && a->grad && rpl__is_gpu(t) && t->grad && add_backward_device_ok(a)) {
+        /* a = x + bias on the device: the ReLU backward's accumulation into
+         * a's gradient runs inside a's add backward pass (same bits). */
+        RplStage s = {0};
+        RplGradSrc src = {1, NULL, NULL, NULL, 0, NULL, 0.0f};
+        src.x = rpl__view_data(&s, a, 1, 0);
+        src.y = rpl__view_grad(&s, t, 1, 0);
+        src.g = rpl__view_grad_acc(&s, a, &src.g_overwrite);
+        rpl__stage_finish(&s);
+        if (!s.err) add_backward_device(a, &src);
+        return;
+    }
     if (a && a->grad) {
         RplStage s = {0};
         int ow = 0;
@@ -256,6 +282,21 @@ void backward_relu(Tensor* t) {
 void backward_mse(Tensor* t) {
     Tensor* pred = t->parent1;
     Tensor* target = t->parent2;
+    if (pred && pred->grad && rpl__is_gpu(t) && rpl__is_gpu(pred) && rpl__is_gpu(target) &&
+        add_backward_device_ok(pred)) {
+        /* pred = x + bias on the device: the MSE backward's accumulation
+         * into pred's gradient runs inside pred's add backward pass (same
+         * bits). */
+        RplStage s = {0};
+        RplGradSrc src = {2, NULL, NULL, NULL, 0, NULL, 0.0f};
+        src.x = rpl__view_data(&s, pred, 1, 0);
+        src.y = rpl__view_data(&s, target, 1, 0);
+        src.g0p = t->size == 1 && rpl__grad_lazy_value(t, &src.g0v) ? NULL : rpl__view_grad(&s, t, 1, 0);
+        src.g = rpl__view_grad_acc(&s, pred, &src.g_overwrite);
+        rpl__stage_finish(&s);
+        if (!s.err) add_backward_device(pred, &src);
+        return;
+    }
     if (pred && pred->grad) {
         RplStage s = {0};
         int ow = 0;

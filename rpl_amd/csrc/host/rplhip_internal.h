@@ -36,8 +36,25 @@ typedef struct {
     void* ws;
     uint64_t splits, nb;
 } RplColsum;
-int rplhip__add_backward_begin(const float* dy, uint64_t n, float* dx, int dx_overwrite, uint64_t nb, RplColsum* cs,
-                               rplhip_stream_t stream);
+/* Where _begin's dy comes from when it is not simply read (src NULL, or
+ * kind 0): the add output's gradient g right after the ReLU (kind 1: x = the
+ * add output's values, y = the ReLU output's gradient) or MSE (kind 2: x =
+ * predictions, y = targets, root gradient *g0p, or g0v when g0p is NULL)
+ * backward that consumes the add accumulated into it.  _begin computes that
+ * accumulation element by element with the same arithmetic, writes g, and
+ * uses the result as dy: the bits of rplhip__relu_backward /
+ * rplhip__mse_backward followed by _begin on g. */
+typedef struct {
+    int kind;
+    const float* x;
+    const float* y;
+    float* g;
+    int g_overwrite;
+    const float* g0p;
+    float g0v;
+} RplGradSrc;
+int rplhip__add_backward_begin(const float* dy, uint64_t n, float* dx, int dx_overwrite, uint64_t nb,
+                               const RplGradSrc* src, RplColsum* cs, rplhip_stream_t stream);
 int rplhip__add_backward_finish(RplColsum* cs, float* db, int db_overwrite, rplhip_stream_t stream);
 
 /* rplhip_sgd_step for up to RPL_SGD_MULTI parameter tensors in one launch

@@ -126,6 +126,18 @@ def check_mlp(orc, r, X, Y, W1, b1, W2, b2):
     assert _rel(r["dW1"], dW1_ref, dH64.T @ np.abs(X64)) <= tol(B)
     _, db1_ref = orc.add_backward(r["dH"], None, np.zeros(H, np.float32))
     assert _rel(r["db1"], db1_ref, dH64.sum(0)) <= tol(B)
+    # The step computes dO and dH inside the bias-gradient passes of the
+    # adds that produced o and h; they must be the bits of the device's own
+    # MSE and ReLU backward kernels on the same tensors.
+    lib = rpl_amd.lib()
+    # (both accumulate: into zeros, the bits of the step's overwrite)
+    do_, dh_ = up(np.zeros(r["o"].size, np.float32)), up(np.zeros(r["h"].size, np.float32))
+    dev_o, dev_y, dev_g0 = up(r["o"]), up(Y), up(np.float32([1.0]))  # held: a freed buffer could be reused
+    rpl_amd.check(lib.rplhip_mse_backward(dev_o.ptr, dev_y.ptr, r["o"].size, dev_g0.ptr, do_.ptr, None))
+    dev_h, dev_da = up(r["h"]), up(r["dA"])
+    rpl_amd.check(lib.rplhip_relu_backward(dev_h.ptr, dev_da.ptr, dh_.ptr, r["h"].size, None))
+    assert bits_equal(r["dO"], down(do_, np.float32, r["o"].shape))
+    assert bits_equal(r["dH"], down(dh_, np.float32, r["h"].shape))
 
 
 def test_mlp_step_golden(gpu, golden, orc):
