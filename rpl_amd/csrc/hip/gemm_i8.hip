@@ -861,7 +861,6 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
 
 namespace dma {
 constexpr int kPairBytes = BM * 2 * BK;  // 256 rows x 128 k-bytes
-constexpr int kPairLoads = 8;            // 1 KB copies per wave per A pair
 }  // namespace dma
 
 template <int EPI, bool BKN>
