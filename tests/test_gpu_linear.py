@@ -140,6 +140,72 @@ def check_mlp(orc, r, X, Y, W1, b1, W2, b2):
     assert bits_equal(r["dH"], down(dh_, np.float32, r["h"].shape))
 
 
+def _two_consumer_graph(lib, X, Y, W1, b1, W2, b2, resident):
+    """h = X W1^T + b1 feeds two ReLUs, each through layer 2; their sum goes
+    into the MSE loss.  Returns every tensor's values and gradients."""
+    B, IN = X.shape
+    H, O = W1.shape[0], W2.shape[0]
+    l1, l2 = lib.linear_create(IN, H), lib.linear_create(H, O)
+    for layer, W, bb in ((l1, W1, b1), (l2, W2, b2)):
+        C.memmove(layer.contents.weight.contents.data, W.ctypes.data, W.nbytes)
+        C.memmove(layer.contents.bias.contents.data, bb.ctypes.data, bb.nbytes)
+    params = [l1.contents.weight, l1.contents.bias, l2.contents.weight, l2.contents.bias]
+    tX, tY = tensor_from(lib, X), tensor_from(lib, Y)
+    if resident:
+        for t in params + [tX, tY]:
+            lib.tensor_to_gpu(t)
+    for t in params:
+        lib.tensor_zero_grad(t)
+    h = lib.linear_forward(l1, tX)
+    a1, a2 = lib.tensor_relu(h), lib.tensor_relu(h)
+    o1, o2 = lib.linear_forward(l2, a1), lib.linear_forward(l2, a2)
+    ssum = lib.tensor_add(o1, o2)
+    loss = lib.tensor_mse_loss(ssum, tY)
+    lib.tensor_backward(loss)
+    err = lib.rpl_last_error()
+    assert not err, err
+    named = dict(loss=(loss, (1,)), s=(ssum, (B, O)), o1=(o1, (B, O)), o2=(o2, (B, O)), a1=(a1, (B, H)),
+                 a2=(a2, (B, H)), h=(h, (B, H)), W1=(params[0], (H, IN)), b1=(params[1], (H,)),
+                 W2=(params[2], (O, H)), b2=(params[3], (O,)))
+    out = {}
+    for k, (t, shape) in named.items():
+        if t.contents.device == rpl_amd.DEVICE_GPU:
+            lib.tensor_from_gpu(t)
+        assert (t.contents.device == rpl_amd.DEVICE_GPU) == resident, k
+        out[k] = host(t, shape)
+        out["d" + k] = host(t, shape, True)
+    for t in (loss, ssum, o2, o1, a2, a1, h, tX, tY):
+        lib.tensor_free(t)
+    lib.linear_free(l1)
+    lib.linear_free(l2)
+    return out
+
+
+def test_fused_backward_matches_staged(gpu):
+    # All tensors GPU-resident, the backward folds the MSE and both ReLU
+    # backwards into the add-backward passes that follow them (h's pass runs
+    # once per ReLU, each time on h's gradient so far, as the reference's
+    # recursion does); with the tensors in host memory every op is staged
+    # and runs the standalone kernels.  Same kernels otherwise, so every
+    # value and gradient must agree bit for bit.
+    lib = gpu
+    B, IN, H, O = 256, 96, 64, 10
+    rng = np.random.default_rng(33)
+    X = rng.uniform(0, 1, (B, IN)).astype(np.float32)
+    Y = rng.uniform(0, 1, (B, O)).astype(np.float32)
+    W1 = rng.uniform(-0.2, 0.2, (H, IN)).astype(np.float32)
+    W2 = rng.uniform(-0.3, 0.3, (O, H)).astype(np.float32)
+    b1 = rng.uniform(-0.1, 0.1, H).astype(np.float32)
+    b2 = rng.uniform(-0.1, 0.1, O).astype(np.float32)
+    say("fused backward vs staged, resident")
+    dev = _two_consumer_graph(lib, X, Y, W1, b1, W2, b2, True)
+    say("fused backward vs staged, host")
+    hst = _two_consumer_graph(lib, X, Y, W1, b1, W2, b2, False)
+    for k in dev:
+        assert bits_equal(dev[k], hst[k]), k
+    assert np.any(dev["dh"] != 0) and np.any(dev["db1"] != 0)
+
+
 def test_mlp_step_golden(gpu, golden, orc):
     X, Y = golden["mlp_X"], golden["mlp_Y"]
     W1, b1, W2, b2 = golden["mlp_W1"], golden["mlp_b1"], golden["mlp_W2"], golden["mlp_b2"]
