@@ -168,6 +168,36 @@ def test_sgemm_wave_split_vs_float64(gpu, M, N, K, ta, tb):
                           np.nan_to_num(C0)) <= fp32_tol(K)
 
 
+def _ws_random_shapes(n, seed_):
+    # Shapes the wave-split kernel takes: N % 4 == 0, M % 4 == 0 and K % 4 == 0
+    # (so every transpose qualifies), K > 256, and either M*N*K <= 2^23 or
+    # too few 128 x 128 tiles to fill the CUs.
+    rng = np.random.default_rng(seed_)
+    out = []
+    while len(out) < n:
+        M = 4 * int(rng.integers(1, 200))
+        N = 4 * int(rng.integers(1, 100))
+        K = 4 * int(rng.integers(65, 3000))
+        tiles = -(-M // 128) * -(-N // 128)
+        if M * N * K <= 1 << 23 or (tiles < 256 and K >= 256):
+            out.append((M, N, K, int(rng.integers(0, 2)), int(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb", _ws_random_shapes(24, 5))
+def test_sgemm_wave_split_random(gpu, M, N, K, ta, tb):
+    rng = np.random.default_rng(M + 3 * N + 7 * K + ta + 2 * tb)
+    A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    alpha, beta = 1.5, 0.25
+    say("sgemm wave split random", M, N, K, ta, tb)
+    out = sgemm(A, B, C0, M, N, K, alpha, beta, ta, tb)
+    opA, opB = op(A, ta).astype(np.float64), op(B, tb).astype(np.float64)
+    ref = alpha * (opA @ opB) + beta * C0.astype(np.float64)
+    assert gemm_err_ratio(out, op(A, ta), op(B, tb), ref, alpha, beta, C0) <= fp32_tol(K)
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_sgemm_wave_split_leading_dimensions(gpu, ta, tb):
     # Sub-matrix views on the wave-split kernel: lda / ldb / ldc past the
