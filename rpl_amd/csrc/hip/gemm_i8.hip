@@ -863,16 +863,17 @@ namespace dma {
 constexpr int kPairBytes = BM * 2 * BK;  // 256 rows x 128 k-bytes
 }  // namespace dma
 
-template <int EPI, bool BKN>
-__global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restrict__ A, uint32_t lda,
-                                                          const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
-                                                          uint32_t N, uint32_t K, EpiParams p) {
+template <int EPI, bool BKN, int BN>
+__device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A, uint32_t lda,
+                                                   const int8_t* __restrict__ B, uint32_t ldb, uint32_t M, uint32_t N,
+                                                   uint32_t K, const EpiParams& p) {
     using dma::BK;
     using dma::BM;
     using dma::kPairBytes;
-    constexpr int BN = 256, S = 4, FN = 4, kLoadsB = 4;
+    static_assert(BN == 256 || (BN == 128 && !BKN), "B tiles of 256 rows, or 128 rows of B [N,K]");
+    constexpr int S = 4, FN = BN / 64, kLoadsB = BN / 64;
     constexpr int kBStage = BN * BK, kBBase = 2 * kPairBytes;
-    constexpr int kReads = BKN ? 12 : 8;  // fragment reads per half
+    constexpr int kReads = BKN ? 12 : 4 + FN;  // fragment reads per half
     __shared__ __attribute__((aligned(1024))) int8_t smem[kBBase + S * kBStage];
 
     const uint32_t lane = threadIdx.x % 64;
@@ -892,7 +893,7 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restri
         for (int j = 0; j < 4; j++)
             boff[j] = (16 * (g / 2) + e) * 256 + ((8 * wn + 2 * j + g % 2) ^ dma::kn_swz(e)) * 16 + 8 * h;
     }
-    using F = dma::HalfFrags<BKN, 4>;
+    using F = dma::HalfFrags<BKN, FN>;
     using dma::lds_v2i;
     v16i acc[4][4];
 
@@ -959,35 +960,49 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restri
                                                             (r - 4) * 32 * BK);
             }
         };
-        // One half: MFMA m on `cur`, then read m of `nxt` (m < kReads) or
-        // copy m - kReads (the half's 4 copies).
-        auto half = [&](const F& cur, F& nxt, uint32_t aslot, uint32_t par, uint32_t stage, int kk, auto copy) {
-            static_for<16>([&](auto Mc) {
+        // One half: its 4*FN MFMAs on `cur`, each followed by the next
+        // memory instruction of the half -- read o of `nxt` (o < kReads),
+        // then copy o - kReads of the half's NC -- with the last MFMAs taking
+        // two when the half has more memory instructions than MFMAs (256 x
+        // 128 tiles: 10 for 8).
+        auto half = [&](const F& cur, F& nxt, uint32_t aslot, uint32_t par, uint32_t stage, int kk, auto NCc,
+                        auto copy) {
+            constexpr int nc = decltype(NCc)::value, nm = 4 * FN, ops = kReads + nc;
+            constexpr int two = ops > nm ? ops - nm : 0;
+            static_for<nm>([&](auto Mc) {
                 constexpr int m = decltype(Mc)::value;
-                acc[m / 4][m % 4] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[m / 4], cur.bv(m % 4),
-                                                                         acc[m / 4][m % 4], 0, 0, 0);
-                if constexpr (m < kReads)
-                    read_one(aslot, par, stage, kk, dma::read_at<BKN, 4>(m), nxt);
-                else if constexpr (m < kReads + 4)
-                    copy(m - kReads);
+                acc[m / FN][m % FN] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[m / FN], cur.bv(m % FN),
+                                                                           acc[m / FN][m % FN], 0, 0, 0);
+                constexpr int first = m < nm - two ? m : (nm - two) + 2 * (m - (nm - two));
+                constexpr int count = m < nm - two ? 1 : 2;
+                static_for<count>([&](auto Oc) {
+                    constexpr int o = first + decltype(Oc)::value;
+                    if constexpr (o < kReads)
+                        read_one(aslot, par, stage, kk, dma::read_at<BKN, FN>(o), nxt);
+                    else if constexpr (o < ops)
+                        copy(o - kReads);
+                });
                 __builtin_amdgcn_sched_barrier(0);
             });
         };
 
         // Prologue: A pair 0 (tiles 0, 1), B tiles 0..2, copies 0..3 of A
-        // pair 1; tile 0 landed.
+        // pair 1; tile 0 landed.  (Copies issued after a tile's last one, at
+        // the wait before it is read: kLoadsB when it is odd (the A copies of
+        // the iteration before and the current B copies), 2 kLoadsB + 4 when
+        // it is even.)
 #pragma unroll
         for (int i = 0; i < 8; i++) copy_a(0, 0, i);
 #pragma unroll
         for (int t = 0; t < 3; t++) {
             const uint32_t src = (uint32_t)t < nks ? t : nks - 1;
 #pragma unroll
-            for (int i = 0; i < 4; i++) copy_b(src, t, i);
+            for (int i = 0; i < kLoadsB; i++) copy_b(src, t, i);
         }
         const uint32_t npairs = nks / 2;
 #pragma unroll
         for (int i = 0; i < 4; i++) copy_a(npairs > 1 ? 1 : 0, 1, i);
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(12, 0));
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kLoadsB + 4, 0));
         __builtin_amdgcn_s_barrier();
         F f0, f1;
         static_for<kReads>([&](auto R) { read_one(0, 0, 0, 0, decltype(R)::value, f0); });
@@ -997,17 +1012,18 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restri
             const uint32_t j = kt + u;
             __builtin_amdgcn_sched_barrier(0);
             const uint32_t tb = j + 3 < nks ? j + 3 : nks - 1;
-            half(f0, f1, (u / 2) % 2, u % 2, u, 1, [&](int c) { copy_b(tb, (u + 3) % S, c); });
-            __builtin_amdgcn_s_waitcnt(waitcnt_imm(u % 2 == 1 ? 4 : 12, 0));
+            half(f0, f1, (u / 2) % 2, u % 2, u, 1, std::integral_constant<int, kLoadsB>{},
+                 [&](int c) { copy_b(tb, (u + 3) % S, c); });
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(u % 2 == 1 ? kLoadsB : 2 * kLoadsB + 4, 0));
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (u % 2 == 1) {
                 const uint32_t pa = (j + 3) / 2 < npairs ? (j + 3) / 2 : npairs - 1;
-                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, (u + 1) % S, 0,
+                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, (u + 1) % S, 0, std::integral_constant<int, 4>{},
                      [&](int c) { copy_a(pa, (u / 2) % 2, c); });
             } else {
                 const uint32_t pa = (j + 2) / 2 < npairs ? (j + 2) / 2 : npairs - 1;
-                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, (u + 1) % S, 0,
+                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, (u + 1) % S, 0, std::integral_constant<int, 4>{},
                      [&](int c) { copy_a(pa, ((u + 2) / 2) % 2, 4 + c); });
             }
         };
@@ -1030,6 +1046,20 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restri
         epilogue_tile_full<EPI, 4, FN, 4>(p, acc, m0 + wm * 128, n0 + wn * (BN / 2), lane);
     else
         epilogue_tile<EPI, 4, FN, 4>(p, acc, m0 + wm * 128 + 4 * (lane / 32), n0 + wn * (BN / 2) + lane % 32, M, N);
+}
+
+template <int EPI, bool BKN>
+__global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs(const int8_t* __restrict__ A, uint32_t lda,
+                                                          const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
+                                                          uint32_t N, uint32_t K, EpiParams p) {
+    gemm_i8_pairs_tile<EPI, BKN, 256>(A, lda, B, ldb, M, N, K, p);
+}
+// 256 x 128 tiles (B [N,K]), for grids with too few 256 x 256 tiles.
+template <int EPI>
+__global__ void __launch_bounds__(256, 1) k_gemm_i8_pairs_n128(const int8_t* __restrict__ A, uint32_t lda,
+                                                               const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
+                                                               uint32_t N, uint32_t K, EpiParams p) {
+    gemm_i8_pairs_tile<EPI, false, 128>(A, lda, B, ldb, M, N, K, p);
 }
 
 // --------------------------------------------------- skinny (M <= 16) GEMM
@@ -1637,8 +1667,12 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
             else
                 hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 256>), dim3(tiles1), dim3(dma::kThreads), 0, s, A, lda, B,
                                    ldb, M, n1, K, p);
-            hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 128>), dim3(tiles2), dim3(dma::kThreads), 0, s, A, lda,
-                               B + (uint64_t)n1 * ldb, ldb, M, N - n1, K, p2);
+            if (use_pairs(K))
+                hipLaunchKernelGGL((k_gemm_i8_pairs_n128<EPI>), dim3(tiles2), dim3(dma::kThreads), 0, s, A,
+                                   lda, B + (uint64_t)n1 * ldb, ldb, M, N - n1, K, p2);
+            else
+                hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 128>), dim3(tiles2), dim3(dma::kThreads), 0, s, A, lda,
+                                   B + (uint64_t)n1 * ldb, ldb, M, N - n1, K, p2);
             return rplhip::check_launch("int8 GEMM (balanced halves)");
         }
         if (dma_ok) {
@@ -1657,8 +1691,12 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
     // give at least 3/4 of a tile per CU (config 3, 2048 x 4096 x 4096: 256).
     const uint64_t tiles_half = mt * ((N + 127) / 128);
     if (dma_ok && use_half_tile() && 4 * tiles_half >= 3ull * rplhip::cu_count()) {
-        hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 128>), dim3((uint32_t)tiles_half), dim3(dma::kThreads), 0, s, A, lda,
-                           B, ldb, M, N, K, p);
+        if (use_pairs(K))
+            hipLaunchKernelGGL((k_gemm_i8_pairs_n128<EPI>), dim3((uint32_t)tiles_half), dim3(dma::kThreads), 0,
+                               s, A, lda, B, ldb, M, N, K, p);
+        else
+            hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 128>), dim3((uint32_t)tiles_half), dim3(dma::kThreads), 0, s, A,
+                               lda, B, ldb, M, N, K, p);
         return rplhip::check_launch("int8 GEMM");
     }
     return launch_nt<CfgSmall, EPI>(A, lda, B, ldb, M, N, K, p, al, s);
