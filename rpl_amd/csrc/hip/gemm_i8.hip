@@ -822,42 +822,53 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
                                      N);
 }
 
-// ------------------- big-tile GEMM with A copied two k-steps at a time
+// ------------------- big-tile GEMM with operands copied two k-steps at a time
 //
-// Same tile (256 x 256 x 64, 4 waves of 128 x 128 on v_mfma_i32_32x32x32_i8),
-// B path and fused epilogues as k_gemm_i8_nt_dma<EPI, 256, BKN>, with A
-// copied in k-step pairs: one copy instruction moves 8 rows x 128 bytes (8
-// whole cache lines; the per-k-step copy moves 16 rows x 64 bytes, half of
-// 16 lines, and fetches each line twice).  A pair of A tiles fills a 32 KB
-// region laid out in 1 KB row groups: group g holds rows 8g..8g+7, the first
-// 512 bytes k-step 2p, the next 512 bytes k-step 2p+1, each as 8 rows x 64
-// bytes with chunk c at slot c ^ swz(row).  Lane l of a copy writes bytes
-// 16l..16l+15 of one group, so it fetches k-step l/32, row 8g + (l%32)/4,
-// chunk (l%4) ^ swz(row).  (Keying the swizzle on row % 8 alone leaves rows
-// 8 apart on the same banks: measured 4 extra cycles per read.)  Fragment
-// reads then see the per-k-step layout (64-byte rows, the same swizzle) at
-// a parity offset of 0 or 512 bytes.  LDS: two A pair slots (64 KB) and
-// four B stages (64 KB).
+// Same tile (256 x BN x 64, 4 waves of 128 x BN/2 on v_mfma_i32_32x32x32_i8)
+// and fused epilogues as k_gemm_i8_nt_dma<EPI, BN, BKN>, with A, and B
+// [N,K], copied in k-step pairs: one copy instruction moves 8 rows x 128
+// bytes (8 whole cache lines; the per-k-step copy moves 16 rows x 64 bytes,
+// half of 16 lines, and fetches each line twice; whole lines copy 1.5-1.75x
+// faster from L2, MALL and HBM alike, measured on MI355X).  A pair of A tiles
+// fills a 32 KB region laid out in 1 KB row groups: group g holds rows
+// 8g..8g+7, the first 512 bytes k-step 2p, the next 512 bytes k-step 2p+1,
+// each as 8 rows x 64 bytes with chunk c at slot c ^ swz(row).  Lane l of a
+// copy writes bytes 16l..16l+15 of one group, so it fetches k-step l/32, row
+// 8g + (l%32)/4, chunk (l%4) ^ swz(row).  (Keying the swizzle on row % 8
+// alone leaves rows 8 apart on the same banks: measured 4 extra cycles per
+// read.)  Fragment reads then see the per-k-step layout (64-byte rows, the
+// same swizzle) at a parity offset of 0 or 512 bytes.  B [N,K] pairs use the
+// same layout over BN rows.  B [K,N] (BKN) keeps the per-k-step stages of
+// k_gemm_i8_nt_dma (its rows are whole 256-byte segments already).  LDS: two
+// A pair slots (64 KB), then four B stages (BKN, 64 KB) or three B pair
+// slots (96 KB at BN = 256, 48 KB at 128).
 //
-// Instruction schedule.  Each 32-k half issues its 16 MFMAs with exactly one
-// other memory instruction after each: the 12 (BKN; 8 for B [N,K]) fragment
-// reads of the next half, then 4 copies.  Copies issued in clusters stall
-// the wave in front of its next MFMA: with the copies bunched, a 64-k step
-// took 1262 cycles against 1024 of MFMA work, spread out 1082 (s_memtime
-// stamps per wave on MI355X, 8192^3).  Iteration j (tile j):
-//   first half:  MFMAs on k-half 0, reads of k-half 1, copies of B tile j+3
-//                into stage (j+3)%4 (tile j-1's, free since the barrier of
-//                iteration j-1);
-//   wait for tile j+1 (vmcnt(4) when j is odd, vmcnt(12) when even), barrier;
+// Instruction schedule.  Each 32-k half issues its 4 FN MFMAs with one other
+// memory instruction after each (two after the last ones when there are
+// more): the 12 (BKN) or 4 + FN fragment reads of the next half, then
+// kLoadsB = BN/64 B copies (first half) or 4 A copies (second half).  Copies
+// issued in clusters stall the wave in front of its next MFMA: with the
+// copies bunched, a 64-k step took 1262 cycles against 1024 of MFMA work,
+// spread out 1082 (s_memtime stamps per wave on MI355X, 8192^3).  Iteration
+// j (tile j):
+//   first half:  MFMAs on k-half 0, reads of k-half 1, and B copies: BKN, B
+//                tile j+3 into stage (j+3)%4 (tile j-1's, free since the
+//                barrier of iteration j-1); B [N,K], copies 0..kLoadsB-1
+//                (j even) or the rest (j odd) of B pair q = j/2 + 2 into slot
+//                q%3 (pair q-3's, free since the barrier of iteration 2q-5);
+//   wait for tile j+1 (vmcnt(kLoadsB) when j is odd, vmcnt(2 kLoadsB + 4)
+//                when even), barrier;
 //   second half: MFMAs on k-half 1, reads of tile j+1's k-half 0, and half
 //                an A pair: j odd, copies 0..3 of pair (j+3)/2 into tile j's
 //                pair slot (free since this barrier); j even, copies 4..7 of
 //                pair (j+2)/2.
-// Every iteration issues the same copies: copies of tiles past the end
-// re-load the last tile (or pair) into a stage or slot that no later read
-// uses, so the wait counts hold to the end and every access stays inside
-// the operands.  Requires K % 128 == 0 and the conditions of
-// k_gemm_i8_nt_dma.
+// A B [N,K] pair is complete two iterations before its first read, and the
+// copy count between two waits is the one of the per-k-step B ring, so the
+// waits are the same for both B layouts.  Every iteration issues the same
+// copies: copies of tiles past the end re-load the last tile (or pair) into
+// a stage or slot that no later read uses, so the wait counts hold to the
+// end and every access stays inside the operands.  Requires K % 128 == 0 and
+// the conditions of k_gemm_i8_nt_dma.
 
 namespace dma {
 constexpr int kPairBytes = BM * 2 * BK;  // 256 rows x 128 k-bytes
@@ -872,9 +883,13 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
     using dma::kPairBytes;
     static_assert(BN == 256 || (BN == 128 && !BKN), "B tiles of 256 rows, or 128 rows of B [N,K]");
     constexpr int S = 4, FN = BN / 64, kLoadsB = BN / 64;
-    constexpr int kBStage = BN * BK, kBBase = 2 * kPairBytes;
+    // B [K,N]: a ring of S k-step stages.  B [N,K]: three k-step pair slots
+    // laid out as A's (BN rows instead of 256).
+    constexpr int kBStage = BN * BK, kBPairBytes = BN * 2 * BK, kBBase = 2 * kPairBytes;
+    constexpr int kBBytes = BKN ? S * kBStage : 3 * kBPairBytes;
+    static_assert(kBBase + kBBytes <= 160 * 1024, "LDS must fit 160 KB");
     constexpr int kReads = BKN ? 12 : 4 + FN;  // fragment reads per half
-    __shared__ __attribute__((aligned(1024))) int8_t smem[kBBase + S * kBStage];
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kBBase + kBBytes];
 
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
@@ -885,7 +900,8 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
 #pragma unroll
     for (int kk = 0; kk < 2; kk++) {
         foff_a[kk] = wm * 16 * 1024 + (fr / 8) * 1024 + (fr % 8) * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
-        foff_b[kk] = wn * (BN / 2) * BK + fr * BK + ((2 * kk + lane / 32) ^ swz(fr)) * 16;
+        foff_b[kk] = (BKN ? wn * (BN / 2) * BK + fr * BK : wn * (BN / 16) * 1024 + (fr / 8) * 1024 + (fr % 8) * BK) +
+                     ((2 * kk + lane / 32) ^ swz(fr)) * 16;
     }
     if constexpr (BKN) {
         const uint32_t g = lane / 16, e = (lane % 16) / 2, h = lane % 2;
@@ -920,44 +936,51 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
                                                      (r < rows_a ? r : rows_a - 1) * lda + (a_col ^ (32 * (i % 2))),
                                                      (k0 + 2 * pair) * BK, 0, 0);
         };
-        // B copies as in k_gemm_i8_nt_dma.
-        uint32_t voff_b[4];
+        // BKN: B copies as in k_gemm_i8_nt_dma, k-step kt into stage `bofs`
+        // (byte offset in the B region).  B [N,K]: copy i of pair `pair` into
+        // the pair slot at `bofs`, laid out as A's: wave w fills row groups
+        // (BN/32)w .. (BN/32)w + BN/32 - 1, copy i rows R = (BN/4)w + 8i +
+        // a_rr (BN/4 is a multiple of 16, so swz(R) = swz(a_rr) ^ 2(i%2) as
+        // for A).
+        uint32_t voff_b[2];
+        if constexpr (BKN) {
 #pragma unroll
-        for (int i = 0; i < kLoadsB; i++) {
-            if constexpr (BKN) {
-                if (i >= 2) continue;
+            for (int i = 0; i < 2; i++) {
                 const uint32_t r = wave * 16 + i * 4 + lane / 16;
                 const uint32_t c = (lane % 16) ^ dma::kn_swz(r % 8);
                 voff_b[i] = r * ldb + (16 * c < rows_b ? c : rows_b / 16 - 1) * 16;
-            } else {
-                const uint32_t r = wave * (BN / 4) + i * 16 + lane / 4;
-                voff_b[i] = (r < rows_b ? r : rows_b - 1) * ldb + ((lane % 4) ^ swz(r)) * 16;
             }
         }
-        auto copy_b = [&](uint32_t kt, uint32_t stage, int i) {
-            int8_t* st = smem + kBBase + stage * kBStage;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr)(st + (wave * (BN / 4) + i * 16) * BK), 16,
-                                                     voff_b[BKN ? i % 2 : i],
-                                                     BKN ? ((k0 + kt) * BK + 8 * (i / 2)) * ldb : (k0 + kt) * BK, 0, 0);
+        auto copy_b = [&](uint32_t kt, uint32_t bofs, int i) {
+            int8_t* st = smem + kBBase + bofs;
+            if constexpr (BKN) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_ptr)(st + (wave * (BN / 4) + i * 16) * BK), 16,
+                                                         voff_b[i % 2], ((k0 + kt) * BK + 8 * (i / 2)) * ldb, 0, 0);
+            } else {
+                const uint32_t r = wave * (BN / 4) + 8 * i + a_rr;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rsrc_b, (lds_ptr)(st + (wave * (BN / 32) + i) * 1024), 16,
+                    (r < rows_b ? r : rows_b - 1) * ldb + (a_col ^ (32 * (i % 2))), (k0 + 2 * kt) * BK, 0, 0);
+            }
         };
-        // Read r of tile (aslot, par, stage), k-half kk: r < 4 is A block r;
-        // then B block (r-4) (B [N,K]) or the low / high transposed half of B
-        // block (r-4)/2 (BKN).
-        auto read_one = [&](uint32_t aslot, uint32_t par, uint32_t stage, int kk, int r, F& f) {
+        // Read r of k-half kk of the k-step at (aslot, par) in A and at byte
+        // offset `bofs` in the B region (BKN: its stage; B [N,K]: its pair
+        // slot plus 512 par): r < 4 is A block r; then B block (r-4) (B
+        // [N,K]) or the low / high transposed half of B block (r-4)/2 (BKN).
+        auto read_one = [&](uint32_t aslot, uint32_t par, uint32_t bofs, int kk, int r, F& f) {
             if (r < 4) {
                 const int8_t* sa_ = smem + aslot * kPairBytes + par * 512 + foff_a[kk];
                 f.a[r] = *reinterpret_cast<const v4i*>(sa_ + r * 4096);
             } else if constexpr (BKN) {
                 const int j = (r - 4) / 2, hi = (r - 4) % 2;
-                const int8_t* pb = smem + kBBase + stage * kBStage + kk * 32 * 256 + boff[j] + hi * 8 * 256;
+                const int8_t* pb = smem + kBBase + bofs + kk * 32 * 256 + boff[j] + hi * 8 * 256;
                 const v2i t = dma::tr8((lds_v2i)pb);
                 if (hi)
                     f.bh[j] = t;
                 else
                     f.bl[j] = t;
             } else {
-                f.b[r - 4] = *reinterpret_cast<const v4i*>(smem + kBBase + stage * kBStage + foff_b[kk] +
-                                                            (r - 4) * 32 * BK);
+                f.b[r - 4] = *reinterpret_cast<const v4i*>(smem + kBBase + bofs + foff_b[kk] + (r - 4) * 4096);
             }
         };
         // One half: its 4*FN MFMAs on `cur`, each followed by the next
@@ -965,7 +988,7 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
         // then copy o - kReads of the half's NC -- with the last MFMAs taking
         // two when the half has more memory instructions than MFMAs (256 x
         // 128 tiles: 10 for 8).
-        auto half = [&](const F& cur, F& nxt, uint32_t aslot, uint32_t par, uint32_t stage, int kk, auto NCc,
+        auto half = [&](const F& cur, F& nxt, uint32_t aslot, uint32_t par, uint32_t bofs, int kk, auto NCc,
                         auto copy) {
             constexpr int nc = decltype(NCc)::value, nm = 4 * FN, ops = kReads + nc;
             constexpr int two = ops > nm ? ops - nm : 0;
@@ -978,7 +1001,7 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
                 static_for<count>([&](auto Oc) {
                     constexpr int o = first + decltype(Oc)::value;
                     if constexpr (o < kReads)
-                        read_one(aslot, par, stage, kk, dma::read_at<BKN, FN>(o), nxt);
+                        read_one(aslot, par, bofs, kk, dma::read_at<BKN, FN>(o), nxt);
                     else if constexpr (o < ops)
                         copy(o - kReads);
                 });
@@ -986,20 +1009,29 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
             });
         };
 
-        // Prologue: A pair 0 (tiles 0, 1), B tiles 0..2, copies 0..3 of A
-        // pair 1; tile 0 landed.  (Copies issued after a tile's last one, at
-        // the wait before it is read: kLoadsB when it is odd (the A copies of
-        // the iteration before and the current B copies), 2 kLoadsB + 4 when
-        // it is even.)
+        // Prologue: A pair 0 (tiles 0, 1), B tiles 0..2 (BKN) or B pairs 0, 1
+        // (slots 0, 1), copies 0..3 of A pair 1; tile 0 landed.  (Copies
+        // issued after a tile's last one, at the wait before it is read:
+        // kLoadsB when it is odd (the A copies of the iteration before and the
+        // current B copies), 2 kLoadsB + 4 when it is even.)
+        const uint32_t npairs = nks / 2;
 #pragma unroll
         for (int i = 0; i < 8; i++) copy_a(0, 0, i);
+        if constexpr (BKN) {
 #pragma unroll
-        for (int t = 0; t < 3; t++) {
-            const uint32_t src = (uint32_t)t < nks ? t : nks - 1;
+            for (int t = 0; t < 3; t++) {
+                const uint32_t src = (uint32_t)t < nks ? t : nks - 1;
 #pragma unroll
-            for (int i = 0; i < kLoadsB; i++) copy_b(src, t, i);
+                for (int i = 0; i < kLoadsB; i++) copy_b(src, t * kBStage, i);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const uint32_t src = (uint32_t)q < npairs ? q : npairs - 1;
+#pragma unroll
+                for (int i = 0; i < 2 * kLoadsB; i++) copy_b(src, q * kBPairBytes, i);
+            }
         }
-        const uint32_t npairs = nks / 2;
 #pragma unroll
         for (int i = 0; i < 4; i++) copy_a(npairs > 1 ? 1 : 0, 1, i);
         __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kLoadsB + 4, 0));
@@ -1007,28 +1039,48 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
         F f0, f1;
         static_for<kReads>([&](auto R) { read_one(0, 0, 0, 0, decltype(R)::value, f0); });
 
+        // B [N,K] pair q lives in slot q % 3; sb = slot of pair kt / 2.
+        uint32_t sb = 0;
+        auto bslot = [&](uint32_t c) {  // byte offset of the slot of pair kt/2 + c, c <= 3
+            const uint32_t s = sb + c;
+            return (s >= 3 ? s - 3 : s) * kBPairBytes;
+        };
         auto iter = [&](auto U, uint32_t kt) {
             constexpr int u = decltype(U)::value;  // kt % 4 == 0
             const uint32_t j = kt + u;
             __builtin_amdgcn_sched_barrier(0);
-            const uint32_t tb = j + 3 < nks ? j + 3 : nks - 1;
-            half(f0, f1, (u / 2) % 2, u % 2, u, 1, std::integral_constant<int, kLoadsB>{},
-                 [&](int c) { copy_b(tb, (u + 3) % S, c); });
+            if constexpr (BKN) {
+                const uint32_t tb = j + 3 < nks ? j + 3 : nks - 1;
+                half(f0, f1, (u / 2) % 2, u % 2, u * kBStage, 1, std::integral_constant<int, kLoadsB>{},
+                     [&](int c) { copy_b(tb, ((u + 3) % S) * kBStage, c); });
+            } else {
+                // Half (u % 2) of B pair kt/2 + u/2 + 2 (copies 0..kLoadsB-1
+                // when j is even, the rest when odd) into its slot, free since
+                // the barrier of iteration j-1 (it held pair kt/2 + u/2 - 1).
+                const uint32_t q = kt / 2 + u / 2 + 2, qb = q < npairs ? q : npairs - 1;
+                const uint32_t dst = bslot(u / 2 + 2);
+                half(f0, f1, (u / 2) % 2, u % 2, bslot(u / 2) + (u % 2) * 512, 1,
+                     std::integral_constant<int, kLoadsB>{}, [&](int c) { copy_b(qb, dst, (u % 2) * kLoadsB + c); });
+            }
             __builtin_amdgcn_s_waitcnt(waitcnt_imm(u % 2 == 1 ? kLoadsB : 2 * kLoadsB + 4, 0));
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
+            const uint32_t bnext = BKN ? ((u + 1) % S) * kBStage : bslot((u + 1) / 2) + ((u + 1) % 2) * 512;
             if constexpr (u % 2 == 1) {
                 const uint32_t pa = (j + 3) / 2 < npairs ? (j + 3) / 2 : npairs - 1;
-                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, (u + 1) % S, 0, std::integral_constant<int, 4>{},
+                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, bnext, 0, std::integral_constant<int, 4>{},
                      [&](int c) { copy_a(pa, (u / 2) % 2, c); });
             } else {
                 const uint32_t pa = (j + 2) / 2 < npairs ? (j + 2) / 2 : npairs - 1;
-                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, (u + 1) % S, 0, std::integral_constant<int, 4>{},
+                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, bnext, 0, std::integral_constant<int, 4>{},
                      [&](int c) { copy_a(pa, ((u + 2) / 2) % 2, 4 + c); });
             }
         };
         uint32_t kt = 0;
-        for (; kt + S <= nks; kt += S) static_for<S>([&](auto U) { iter(U, kt); });
+        for (; kt + S <= nks; kt += S) {
+            static_for<S>([&](auto U) { iter(U, kt); });
+            sb = sb == 0 ? 2 : sb - 1;  // + 2 pairs
+        }
         if (kt < nks) static_for<2>([&](auto U) { iter(U, kt); });  // nks % 4 == 2
         // The trailing copies land before the LDS is reused or released.
         __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
