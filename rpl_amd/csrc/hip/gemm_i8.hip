@@ -71,20 +71,44 @@ struct EpiParams {
     uint32_t ldc;
 };
 
-// Output bits of element (m, n) from its accumulator.  cadd / cmul / rmul
-// are the per-column bias, per-column and per-row dequant scales when the
-// caller has them at hand (kRaw / kDequant); the float operation order is
-// the reference's (src/ops_extended.c:119).
+// The column and row terms of the epilogue, loaded once per column / row by
+// the tile epilogues: cadd (kRaw: bias[n]; kRequant: -za * rowsum_b[n]),
+// cmul (kDequant: sw[n]), radd (kRequant: -zb * rowsum_a[m]) and rmul
+// (kDequant: sx[m]); 0 where the variant has none.
 template <int EPI>
-__device__ __forceinline__ uint32_t epi_bits(const EpiParams& p, int32_t acc, uint32_t m, uint32_t n, int32_t cadd,
-                                             float rmul, float cmul) {
+__device__ __forceinline__ int32_t epi_cadd(const EpiParams& p, uint32_t n) {
+    if constexpr (EPI == kRaw) return p.bias ? (int32_t)p.bias[n] : 0;
+    if constexpr (EPI == kRequant) return p.rowsum_b ? -wrap_mul(p.za, p.rowsum_b[n]) : 0;
+    return 0;
+}
+template <int EPI>
+__device__ __forceinline__ float epi_cmul(const EpiParams& p, uint32_t n) {
+    if constexpr (EPI == kDequant) return p.sw[p.sw_per_col ? n : 0];
+    return 0.0f;
+}
+template <int EPI>
+__device__ __forceinline__ int32_t epi_radd(const EpiParams& p, uint32_t m) {
+    if constexpr (EPI == kRequant) return p.rowsum_a ? -wrap_mul(p.zb, p.rowsum_a[m]) : 0;
+    return 0;
+}
+template <int EPI>
+__device__ __forceinline__ float epi_rmul(const EpiParams& p, uint32_t m) {
+    if constexpr (EPI == kDequant) return p.sx[p.sx_per_row ? m : 0];
+    return 0.0f;
+}
+
+// Output bits of one element from its accumulator and the terms of its
+// column (cadd, cmul) and row (radd, rmul); the int32 sums wrap, so their
+// order does not matter, and the float operation order is the reference's
+// (src/ops_extended.c:119).
+template <int EPI>
+__device__ __forceinline__ uint32_t epi_bits(const EpiParams& p, int32_t acc, int32_t cadd, float cmul, int32_t radd,
+                                             float rmul) {
 #pragma clang fp contract(off)
     if constexpr (EPI == kRaw) {
         return (uint32_t)wrap_add(acc, cadd);
     } else if constexpr (EPI == kRequant) {
-        int32_t v = acc;
-        if (p.rowsum_a) v = wrap_add(v, -wrap_mul(p.zb, p.rowsum_a[m]));
-        if (p.rowsum_b) v = wrap_add(v, -wrap_mul(p.za, p.rowsum_b[n]));
+        int32_t v = wrap_add(wrap_add(acc, radd), cadd);
         v = wrap_add(v, p.kzz);
         return (uint32_t)x86_round_cvt((float)v * p.sa * p.sb / p.sc);
     } else if constexpr (EPI == kRequantPow2) {
@@ -101,10 +125,8 @@ __device__ __forceinline__ uint32_t epi_bits(const EpiParams& p, int32_t acc, ui
 template <int EPI>
 __device__ __forceinline__ void epilogue_store(const EpiParams& p, uint32_t m, uint32_t n, int32_t acc) {
     const uint64_t o = (uint64_t)m * p.ldc + n;
-    const int32_t cadd = (EPI == kRaw && p.bias) ? (int32_t)p.bias[n] : 0;
-    const float rmul = EPI == kDequant ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
-    const float cmul = EPI == kDequant ? p.sw[p.sw_per_col ? n : 0] : 0.0f;
-    const uint32_t bits = epi_bits<EPI>(p, acc, m, n, cadd, rmul, cmul);
+    const uint32_t bits = epi_bits<EPI>(p, acc, epi_cadd<EPI>(p, n), epi_cmul<EPI>(p, n), epi_radd<EPI>(p, m),
+                                        epi_rmul<EPI>(p, m));
     if constexpr (EPI == kDequant)
         p.out_f32[o] = __uint_as_float(bits);
     else
@@ -198,14 +220,12 @@ __device__ __forceinline__ void epilogue_store4(const EpiParams& p, uint32_t m, 
     const uint64_t o = (uint64_t)m * p.ldc + n;
     void* out = EPI == kDequant ? (void*)(p.out_f32 + o) : (void*)(p.out_i32 + o);
     if (n + 3 < N && (p.ldc & 3) == 0 && (((uintptr_t)out) & 15) == 0) {
-        const float rmul = EPI == kDequant ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
+        const int32_t radd = epi_radd<EPI>(p, m);
+        const float rmul = epi_rmul<EPI>(p, m);
         v4i r;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int32_t cadd = (EPI == kRaw && p.bias) ? (int32_t)p.bias[n + e] : 0;
-            const float cmul = EPI == kDequant ? p.sw[p.sw_per_col ? n + e : 0] : 0.0f;
-            r[e] = (int32_t)epi_bits<EPI>(p, v[e], m, n + e, cadd, rmul, cmul);
-        }
+        for (int e = 0; e < 4; e++)
+            r[e] = (int32_t)epi_bits<EPI>(p, v[e], epi_cadd<EPI>(p, n + e), epi_cmul<EPI>(p, n + e), radd, rmul);
         *reinterpret_cast<v4i*>(out) = r;
     } else {
 #pragma unroll
@@ -411,26 +431,38 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt(const int8_t* __restrict_
 template <int EPI, int FM, int FN, int FNA = FN>
 __device__ __forceinline__ void epilogue_tile(const EpiParams& p, const v16i (&acc)[FM][FNA], uint32_t mb,
                                               uint32_t nb, uint32_t M, uint32_t N) {
-    int32_t cadd[FN];  // kRaw: bias[n]
-    float cmul[FN];    // kDequant: sw[n]
+    int32_t cadd[FN];
+    float cmul[FN];
 #pragma unroll
     for (int j = 0; j < FN; j++) {
         const uint32_t n = nb + j * 32;
-        cadd[j] = (EPI == kRaw && p.bias && n < N) ? (int32_t)p.bias[n] : 0;
-        cmul[j] = (EPI == kDequant && n < N) ? p.sw[p.sw_per_col ? n : 0] : 0.0f;
+        cadd[j] = n < N ? epi_cadd<EPI>(p, n) : 0;
+        cmul[j] = n < N ? epi_cmul<EPI>(p, n) : 0.0f;
     }
+    // The row terms of all the lane's rows before the first store (stores
+    // count in vmcnt: a load between them would wait for every earlier one).
+    int32_t radd[FM][16];
+    float rmul[FM][16];
+    static_for<FM>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        static_for<16>([&](auto R) {
+            constexpr int r = decltype(R)::value;
+            const uint32_t m = mb + i * 32 + 8 * (r / 4) + r % 4;
+            radd[i][r] = m < M ? epi_radd<EPI>(p, m) : 0;
+            rmul[i][r] = m < M ? epi_rmul<EPI>(p, m) : 0.0f;
+        });
+    });
     static_for<FM>([&](auto I) {
         constexpr int i = decltype(I)::value;
         static_for<16>([&](auto R) {
             constexpr int r = decltype(R)::value;
             const uint32_t m = mb + i * 32 + 8 * (r / 4) + r % 4;
             if (m >= M) return;
-            const float rmul = EPI == kDequant ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
             static_for<FN>([&](auto J) {
                 constexpr int j = decltype(J)::value;
                 const uint32_t n = nb + j * 32;
                 if (n < N) {
-                    const uint32_t bits = epi_bits<EPI>(p, acc[i][j][r], m, n, cadd[j], rmul, cmul[j]);
+                    const uint32_t bits = epi_bits<EPI>(p, acc[i][j][r], cadd[j], cmul[j], radd[i][r], rmul[i][r]);
                     const uint64_t o = (uint64_t)m * p.ldc + n;
                     if constexpr (EPI == kDequant)
                         p.out_f32[o] = __uint_as_float(bits);
@@ -472,21 +504,30 @@ __device__ __forceinline__ void epilogue_tile_full(const EpiParams& p, const v16
     float cmul[FN];
 #pragma unroll
     for (int j = 0; j < FN; j++) {
-        const uint32_t n = nb + j * 32;
-        cadd[j] = (EPI == kRaw && p.bias) ? (int32_t)p.bias[n] : 0;
-        cmul[j] = EPI == kDequant ? p.sw[p.sw_per_col ? n : 0] : 0.0f;
+        cadd[j] = epi_cadd<EPI>(p, nb + j * 32);
+        cmul[j] = epi_cmul<EPI>(p, nb + j * 32);
     }
+    // The row terms of all the lane's rows before the first store (stores
+    // count in vmcnt: a load between them would wait for every earlier one).
+    int32_t radd[FM][16];
+    float rmul[FM][16];
+    static_for<FM>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        static_for<16>([&](auto R) {
+            constexpr int r = decltype(R)::value;
+            radd[i][r] = epi_radd<EPI>(p, mb + i * 32 + 8 * (r / 4) + r % 4);
+            rmul[i][r] = epi_rmul<EPI>(p, mb + i * 32 + 8 * (r / 4) + r % 4);
+        });
+    });
     static_for<FM>([&](auto I) {
         constexpr int i = decltype(I)::value;
         static_for<16>([&](auto R) {
             constexpr int r = decltype(R)::value;
             constexpr uint32_t row = i * 32 + 8 * (r / 4) + r % 4;
-            const uint32_t m = mb + row;
-            const float rmul = EPI == kDequant ? p.sx[p.sx_per_row ? m : 0] : 0.0f;
             const int soff = (int)__builtin_amdgcn_readfirstlane(row * ldc4);
             static_for<FN>([&](auto J) {
                 constexpr int j = decltype(J)::value;
-                const uint32_t bits = epi_bits<EPI>(p, acc[i][j][r], m, nb + j * 32, cadd[j], rmul, cmul[j]);
+                const uint32_t bits = epi_bits<EPI>(p, acc[i][j][r], cadd[j], cmul[j], radd[i][r], rmul[i][r]);
                 __builtin_amdgcn_raw_buffer_store_b32(bits, rsrc, (int)(voff + j * 128), soff, RPL_I8_EPI_CPOL);
             });
         });
