@@ -214,23 +214,52 @@ struct Frags {
     v4i a[G::FM], b[G::FN];
 };
 
-// Fused epilogue on 4 consecutive columns n..n+3 of row m.
+// Fused epilogue of rows m0..m0+3 of column n (a lane's 4 results of a
+// 16 x 16 MFMA block), with the terms loaded before the first store (stores
+// count in vmcnt: a load between them would wait for every earlier one).
 template <int EPI>
-__device__ __forceinline__ void epilogue_store4(const EpiParams& p, uint32_t m, uint32_t n, uint32_t N, v4i v) {
+__device__ __forceinline__ void epilogue_store_rows4(const EpiParams& p, uint32_t m0, uint32_t n, uint32_t M,
+                                                     uint32_t N, v4i v) {
+    if (n >= N) return;
+    const int32_t cadd = epi_cadd<EPI>(p, n);
+    const float cmul = epi_cmul<EPI>(p, n);
+    int32_t radd[4];
+    float rmul[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {  // rows past M read row M-1, never stored
+        radd[r] = epi_radd<EPI>(p, m0 + r < M ? m0 + r : M - 1);
+        rmul[r] = epi_rmul<EPI>(p, m0 + r < M ? m0 + r : M - 1);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));  // the stores below need no vmcnt wait
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        if (m0 + r >= M) break;
+        const uint64_t o = (uint64_t)(m0 + r) * p.ldc + n;
+        const uint32_t bits = epi_bits<EPI>(p, v[r], cadd, cmul, radd[r], rmul[r]);
+        if constexpr (EPI == kDequant)
+            p.out_f32[o] = __uint_as_float(bits);
+        else
+            p.out_i32[o] = (int32_t)bits;
+    }
+}
+
+// Fused epilogue on 4 consecutive columns n..n+3 of row m, given the
+// columns' and the row's terms.
+template <int EPI>
+__device__ __forceinline__ void epilogue_store4(const EpiParams& p, uint32_t m, uint32_t n, uint32_t N, v4i v,
+                                                const int32_t (&cadd)[4], const float (&cmul)[4], int32_t radd,
+                                                float rmul) {
     const uint64_t o = (uint64_t)m * p.ldc + n;
     void* out = EPI == kDequant ? (void*)(p.out_f32 + o) : (void*)(p.out_i32 + o);
-    if (n + 3 < N && (p.ldc & 3) == 0 && (((uintptr_t)out) & 15) == 0) {
-        const int32_t radd = epi_radd<EPI>(p, m);
-        const float rmul = epi_rmul<EPI>(p, m);
-        v4i r;
+    v4i r;
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-            r[e] = (int32_t)epi_bits<EPI>(p, v[e], epi_cadd<EPI>(p, n + e), epi_cmul<EPI>(p, n + e), radd, rmul);
+    for (int e = 0; e < 4; e++) r[e] = (int32_t)epi_bits<EPI>(p, v[e], cadd[e], cmul[e], radd, rmul);
+    if (n + 3 < N && (p.ldc & 3) == 0 && (((uintptr_t)out) & 15) == 0) {
         *reinterpret_cast<v4i*>(out) = r;
     } else {
 #pragma unroll
         for (int e = 0; e < 4; e++)
-            if (n + e < N) epilogue_store<EPI>(p, m, n + e, v[e]);
+            if (n + e < N) reinterpret_cast<int32_t*>(out)[e] = r[e];
     }
 }
 
@@ -399,6 +428,30 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt(const int8_t* __restrict_
     // is a compile-time constant (static_for), so the accumulators are never
     // indexed dynamically (which would force them out of registers).
     int32_t* stage = reinterpret_cast<int32_t*>(smem) + wave * 32 * G::kEpiPitch;
+    constexpr int kLanesPerRow = TN / 4;
+    constexpr int kRowsPerPass = 64 / kLanesPerRow, kPasses = 32 / kRowsPerPass;
+    const uint32_t row0 = lane / kLanesPerRow, col = (lane % kLanesPerRow) * 4, n = n0 + wn * TN + col;
+    // The column and row terms of every element the lane stores, all
+    // loaded and waited for before the first store (stores count in vmcnt:
+    // a load between them, or a wait the compiler cannot count through the
+    // stores' branches, would wait for every earlier store).  Columns and
+    // rows past N and M read the last one, never stored.
+    int32_t cadd[4], radd[FM][kPasses];
+    float cmul[4], rmul[FM][kPasses];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        cadd[e] = epi_cadd<EPI>(p, n + e < N ? n + e : N - 1);
+        cmul[e] = epi_cmul<EPI>(p, n + e < N ? n + e : N - 1);
+    }
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int k = 0; k < kPasses; k++) {
+            const uint32_t m = m0 + wm * TM + i * 32 + k * kRowsPerPass + row0;
+            radd[i][k] = epi_radd<EPI>(p, m < M ? m : M - 1);
+            rmul[i][k] = epi_rmul<EPI>(p, m < M ? m : M - 1);
+        }
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
     static_for<FM>([&](auto I) {
         constexpr int i = decltype(I)::value;
 #pragma unroll
@@ -407,13 +460,12 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt(const int8_t* __restrict_
             for (int r = 0; r < 16; r++)
                 stage[(8 * (r / 4) + 4 * (lane / 32) + r % 4) * G::kEpiPitch + j * 32 + lane % 32] = acc[i][j][r];
         __syncthreads();
-        constexpr int kLanesPerRow = TN / 4;
-        constexpr int kRowsPerPass = 64 / kLanesPerRow;
-        for (int rr = 0; rr < 32; rr += kRowsPerPass) {
-            const uint32_t row = rr + lane / kLanesPerRow, col = (lane % kLanesPerRow) * 4;
+#pragma unroll
+        for (int k = 0; k < kPasses; k++) {
+            const uint32_t row = k * kRowsPerPass + row0;
             const v4i v = *reinterpret_cast<const v4i*>(&stage[row * G::kEpiPitch + col]);
-            const uint32_t m = m0 + wm * TM + i * 32 + row, n = n0 + wn * TN + col;
-            if (m < M && n < N) epilogue_store4<EPI>(p, m, n, N, v);
+            const uint32_t m = m0 + wm * TM + i * 32 + row;
+            if (m < M && n < N) epilogue_store4<EPI>(p, m, n, N, v, cadd, cmul, radd[i][k], rmul[i][k]);
         }
         __syncthreads();
     });
@@ -431,16 +483,19 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt(const int8_t* __restrict_
 template <int EPI, int FM, int FN, int FNA = FN>
 __device__ __forceinline__ void epilogue_tile(const EpiParams& p, const v16i (&acc)[FM][FNA], uint32_t mb,
                                               uint32_t nb, uint32_t M, uint32_t N) {
+    // The column and row terms of all the lane's elements, loaded and
+    // waited for before the first store (stores count in vmcnt: a load
+    // between them, or a wait the compiler cannot count through the stores'
+    // bounds branches, would wait for every earlier store).  Columns and
+    // rows past N and M read the last one, never stored.
     int32_t cadd[FN];
     float cmul[FN];
 #pragma unroll
     for (int j = 0; j < FN; j++) {
         const uint32_t n = nb + j * 32;
-        cadd[j] = n < N ? epi_cadd<EPI>(p, n) : 0;
-        cmul[j] = n < N ? epi_cmul<EPI>(p, n) : 0.0f;
+        cadd[j] = epi_cadd<EPI>(p, n < N ? n : N - 1);
+        cmul[j] = epi_cmul<EPI>(p, n < N ? n : N - 1);
     }
-    // The row terms of all the lane's rows before the first store (stores
-    // count in vmcnt: a load between them would wait for every earlier one).
     int32_t radd[FM][16];
     float rmul[FM][16];
     static_for<FM>([&](auto I) {
@@ -448,10 +503,11 @@ __device__ __forceinline__ void epilogue_tile(const EpiParams& p, const v16i (&a
         static_for<16>([&](auto R) {
             constexpr int r = decltype(R)::value;
             const uint32_t m = mb + i * 32 + 8 * (r / 4) + r % 4;
-            radd[i][r] = m < M ? epi_radd<EPI>(p, m) : 0;
-            rmul[i][r] = m < M ? epi_rmul<EPI>(p, m) : 0.0f;
+            radd[i][r] = epi_radd<EPI>(p, m < M ? m : M - 1);
+            rmul[i][r] = epi_rmul<EPI>(p, m < M ? m : M - 1);
         });
     });
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
     static_for<FM>([&](auto I) {
         constexpr int i = decltype(I)::value;
         static_for<16>([&](auto R) {
@@ -1206,11 +1262,7 @@ __global__ void __launch_bounds__(kSkThreads) k_gemv_i8_nt(const int8_t* __restr
         s[2] = wrap_add(s[2], t[2]);
         s[3] = wrap_add(s[3], t[3]);
     }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        uint32_t m = 4 * (lane / 16) + r, n = n0 + q * 16 + lane % 16;
-        if (m < M && n < N) epilogue_store<EPI>(p, m, n, s[r]);
-    }
+    epilogue_store_rows4<EPI>(p, 4 * (lane / 16), n0 + q * 16 + lane % 16, M, N, s);
 }
 
 // ---------------------------------------------------- skinny (M <= 16) GEMM
@@ -1362,11 +1414,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_skinny(const int8_t* __restrict_
         for (int e = 0; e < 4; e++) t[e] = wrap_add(t[e], u[e]);
     }
     // Result element r of lane l: row 4*(l/16) + r, column l%16 of the panel.
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const uint32_t m = 4 * (lane / 16) + r, n = n0 + 16 * wave + lane % 16;
-        if (m < M && n < N) epilogue_store<EPI>(p, m, n, t[r]);
-    }
+    epilogue_store_rows4<EPI>(p, 4 * (lane / 16), n0 + 16 * wave + lane % 16, M, N, t);
 }
 
 // ------------------------------------------- decode-sized (M <= 4) GEMM
