@@ -506,6 +506,41 @@ __global__ void __launch_bounds__(256, 1) k_sgemm_dma(uint32_t M, uint32_t N, ui
     const uint32_t mw = m0 + wm * 128, nw = n0 + wn * 128;
     const bool full = m0 + BM <= M && n0 + BN <= N;
     auto row_m = [&](int i, int r) { return mw + OpA::row(i, 8 * (r / 4) + 4 * (lane / 32) + r % 4); };
+    if constexpr (!TB) {
+        if (full && read_c) {
+            // Interior tile, in units of 8 rows (half a row block): unit
+            // u+1's C reads are issued before unit u's stores, so each
+            // unit's reads wait only for the stores of the unit two back
+            // (stores count in vmcnt).  The units are distinct rows of C
+            // (ldc >= N).  Two units in flight keep 64 VGPRs of C, as one
+            // whole row block does.
+            const uint32_t n = nw + 4 * (lane % 32);
+            float4 cv[2][8];
+            auto load_c = [&](auto U) {
+                constexpr int u = decltype(U)::value;
+#pragma unroll
+                for (int r = 0; r < 8; r++)
+                    cv[u % 2][r] =
+                        *reinterpret_cast<const float4*>(C + (uint64_t)row_m(u / 2, 8 * (u % 2) + r) * ldc + n);
+            };
+            load_c(std::integral_constant<int, 0>{});
+            static_for<8>([&](auto U) {
+                constexpr int u = decltype(U)::value, i = u / 2;
+                if constexpr (u + 1 < 8) load_c(std::integral_constant<int, u + 1>{});
+#pragma unroll
+                for (int r = 0; r < 8; r++) {
+                    const int rr = 8 * (u % 2) + r;
+                    float4 c = cv[u % 2][r];
+                    c.x = alpha * acc[i][0][rr] + beta * c.x;
+                    c.y = alpha * acc[i][1][rr] + beta * c.y;
+                    c.z = alpha * acc[i][2][rr] + beta * c.z;
+                    c.w = alpha * acc[i][3][rr] + beta * c.w;
+                    *reinterpret_cast<float4*>(C + (uint64_t)row_m(i, rr) * ldc + n) = c;
+                }
+            });
+            return;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if (!TB) {
