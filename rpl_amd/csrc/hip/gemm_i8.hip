@@ -982,7 +982,10 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
     constexpr int S = 4, FN = BN / 64, kLoadsB = BN / 64;
     // B [K,N]: a ring of S k-step stages.  B [N,K]: three k-step pair slots
     // laid out as A's (BN rows instead of 256).
-    constexpr int kBStage = BN * BK, kBPairBytes = BN * 2 * BK, kBBase = 2 * kPairBytes;
+    // A pair slots: three for 256 x 128 tiles, whose LDS has room (their A
+    // copies then start two k-steps earlier), two for 256 x 256.
+    constexpr int kASlots = BN == 128 ? 3 : 2;
+    constexpr int kBStage = BN * BK, kBPairBytes = BN * 2 * BK, kBBase = kASlots * kPairBytes;
     constexpr int kBBytes = BKN ? S * kBStage : 3 * kBPairBytes;
     static_assert(kBBase + kBBytes <= 160 * 1024, "LDS must fit 160 KB");
     constexpr int kReads = BKN ? 12 : 4 + FN;  // fragment reads per half
@@ -1026,8 +1029,8 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
         const uint32_t a_rr = (lane % 32) / 4;
         const uint32_t a_row = wave * 64 + a_rr;
         const uint32_t a_col = (lane / 32) * BK + ((lane % 4) ^ swz(a_rr)) * 16;
-        auto copy_a = [&](uint32_t pair, int slot, int i) {
-            int8_t* st = smem + slot * kPairBytes + wave * 8 * 1024;
+        auto copy_a = [&](uint32_t pair, uint32_t aofs, int i) {  // aofs: the slot's byte offset
+            int8_t* st = smem + aofs + wave * 8 * 1024;
             const uint32_t r = a_row + 8 * i;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_ptr)(st + i * 1024), 16,
                                                      (r < rows_a ? r : rows_a - 1) * lda + (a_col ^ (32 * (i % 2))),
@@ -1060,13 +1063,14 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
                     (r < rows_b ? r : rows_b - 1) * ldb + (a_col ^ (32 * (i % 2))), (k0 + 2 * kt) * BK, 0, 0);
             }
         };
-        // Read r of k-half kk of the k-step at (aslot, par) in A and at byte
-        // offset `bofs` in the B region (BKN: its stage; B [N,K]: its pair
-        // slot plus 512 par): r < 4 is A block r; then B block (r-4) (B
-        // [N,K]) or the low / high transposed half of B block (r-4)/2 (BKN).
-        auto read_one = [&](uint32_t aslot, uint32_t par, uint32_t bofs, int kk, int r, F& f) {
+        // Read r of k-half kk of the k-step at parity par of the A pair slot
+        // at byte offset aofs and at byte offset `bofs` in the B region (BKN:
+        // its stage; B [N,K]: its pair slot plus 512 par): r < 4 is A block
+        // r; then B block (r-4) (B [N,K]) or the low / high transposed half
+        // of B block (r-4)/2 (BKN).
+        auto read_one = [&](uint32_t aofs, uint32_t par, uint32_t bofs, int kk, int r, F& f) {
             if (r < 4) {
-                const int8_t* sa_ = smem + aslot * kPairBytes + par * 512 + foff_a[kk];
+                const int8_t* sa_ = smem + aofs + par * 512 + foff_a[kk];
                 f.a[r] = *reinterpret_cast<const v4i*>(sa_ + r * 4096);
             } else if constexpr (BKN) {
                 const int j = (r - 4) / 2, hi = (r - 4) % 2;
@@ -1085,7 +1089,7 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
         // then copy o - kReads of the half's NC -- with the last MFMAs taking
         // two when the half has more memory instructions than MFMAs (256 x
         // 128 tiles: 10 for 8).
-        auto half = [&](const F& cur, F& nxt, uint32_t aslot, uint32_t par, uint32_t bofs, int kk, auto NCc,
+        auto half = [&](const F& cur, F& nxt, uint32_t aofs, uint32_t par, uint32_t bofs, int kk, auto NCc,
                         auto copy) {
             constexpr int nc = decltype(NCc)::value, nm = 4 * FN, ops = kReads + nc;
             constexpr int two = ops > nm ? ops - nm : 0;
@@ -1098,7 +1102,7 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
                 static_for<count>([&](auto Oc) {
                     constexpr int o = first + decltype(Oc)::value;
                     if constexpr (o < kReads)
-                        read_one(aslot, par, bofs, kk, dma::read_at<BKN, FN>(o), nxt);
+                        read_one(aofs, par, bofs, kk, dma::read_at<BKN, FN>(o), nxt);
                     else if constexpr (o < ops)
                         copy(o - kReads);
                 });
@@ -1107,11 +1111,16 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
         };
 
         // Prologue: A pair 0 (tiles 0, 1), B tiles 0..2 (BKN) or B pairs 0, 1
-        // (slots 0, 1), copies 0..3 of A pair 1; tile 0 landed.  (Copies
-        // issued after a tile's last one, at the wait before it is read:
-        // kLoadsB when it is odd (the A copies of the iteration before and the
-        // current B copies), 2 kLoadsB + 4 when it is even.)
+        // (slots 0, 1), then copies 0..3 of A pair 1 (two A slots) or all of
+        // A pair 1 and copies 0..3 of A pair 2 (three); tile 0 landed.  The
+        // waits before a tile's first read allow the copies issued after its
+        // last one: with two A slots kLoadsB when the tile is even (the A
+        // copies of the iteration before and the current B copies) and
+        // 2 kLoadsB + 4 when odd; with three (B binds: its last copies are
+        // two iterations back) 2 kLoadsB + 8 and 3 kLoadsB + 12.
         const uint32_t npairs = nks / 2;
+        constexpr int kWaitEvenTile = kASlots == 3 ? 2 * kLoadsB + 8 : kLoadsB;
+        constexpr int kWaitOddTile = kASlots == 3 ? 3 * kLoadsB + 12 : 2 * kLoadsB + 4;
 #pragma unroll
         for (int i = 0; i < 8; i++) copy_a(0, 0, i);
         if constexpr (BKN) {
@@ -1129,26 +1138,37 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
                 for (int i = 0; i < 2 * kLoadsB; i++) copy_b(src, q * kBPairBytes, i);
             }
         }
+        if constexpr (kASlots == 3) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) copy_a(npairs > 1 ? 1 : 0, 1, i);
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kLoadsB + 4, 0));
+            for (int i = 0; i < 8; i++) copy_a(npairs > 1 ? 1 : 0, kPairBytes, i);
+#pragma unroll
+            for (int i = 0; i < 4; i++) copy_a(npairs > 2 ? 2 : npairs - 1, 2 * kPairBytes, i);
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kLoadsB + 12, 0));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) copy_a(npairs > 1 ? 1 : 0, kPairBytes, i);
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * kLoadsB + 4, 0));
+        }
         __builtin_amdgcn_s_barrier();
         F f0, f1;
         static_for<kReads>([&](auto R) { read_one(0, 0, 0, 0, decltype(R)::value, f0); });
 
-        // B [N,K] pair q lives in slot q % 3; sb = slot of pair kt / 2.
+        // With three slots, pair q (A or B [N,K]) lives in slot q % 3; sb =
+        // the slot of pair kt / 2.  With two A slots, A pair q in slot q % 2.
         uint32_t sb = 0;
-        auto bslot = [&](uint32_t c) {  // byte offset of the slot of pair kt/2 + c, c <= 3
-            const uint32_t s = sb + c;
-            return (s >= 3 ? s - 3 : s) * kBPairBytes;
+        auto slot3 = [&](uint32_t c) {  // slot of pair kt/2 + c, c <= 4
+            const uint32_t s = sb + c, t = s >= 3 ? s - 3 : s;
+            return t >= 3 ? t - 3 : t;
         };
+        auto bslot = [&](uint32_t c) { return slot3(c) * kBPairBytes; };
+        auto aslot = [&](uint32_t c) { return (kASlots == 3 ? slot3(c) : c % 2) * kPairBytes; };
         auto iter = [&](auto U, uint32_t kt) {
             constexpr int u = decltype(U)::value;  // kt % 4 == 0
             const uint32_t j = kt + u;
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (BKN) {
                 const uint32_t tb = j + 3 < nks ? j + 3 : nks - 1;
-                half(f0, f1, (u / 2) % 2, u % 2, u * kBStage, 1, std::integral_constant<int, kLoadsB>{},
+                half(f0, f1, aslot(u / 2), u % 2, u * kBStage, 1, std::integral_constant<int, kLoadsB>{},
                      [&](int c) { copy_b(tb, ((u + 3) % S) * kBStage, c); });
             } else {
                 // Half (u % 2) of B pair kt/2 + u/2 + 2 (copies 0..kLoadsB-1
@@ -1156,22 +1176,21 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
                 // the barrier of iteration j-1 (it held pair kt/2 + u/2 - 1).
                 const uint32_t q = kt / 2 + u / 2 + 2, qb = q < npairs ? q : npairs - 1;
                 const uint32_t dst = bslot(u / 2 + 2);
-                half(f0, f1, (u / 2) % 2, u % 2, bslot(u / 2) + (u % 2) * 512, 1,
+                half(f0, f1, aslot(u / 2), u % 2, bslot(u / 2) + (u % 2) * 512, 1,
                      std::integral_constant<int, kLoadsB>{}, [&](int c) { copy_b(qb, dst, (u % 2) * kLoadsB + c); });
             }
-            __builtin_amdgcn_s_waitcnt(waitcnt_imm(u % 2 == 1 ? kLoadsB : 2 * kLoadsB + 4, 0));
+            __builtin_amdgcn_s_waitcnt(waitcnt_imm(u % 2 == 1 ? kWaitEvenTile : kWaitOddTile, 0));
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
             const uint32_t bnext = BKN ? ((u + 1) % S) * kBStage : bslot((u + 1) / 2) + ((u + 1) % 2) * 512;
-            if constexpr (u % 2 == 1) {
-                const uint32_t pa = (j + 3) / 2 < npairs ? (j + 3) / 2 : npairs - 1;
-                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, bnext, 0, std::integral_constant<int, 4>{},
-                     [&](int c) { copy_a(pa, (u / 2) % 2, c); });
-            } else {
-                const uint32_t pa = (j + 2) / 2 < npairs ? (j + 2) / 2 : npairs - 1;
-                half(f1, f0, ((u + 1) / 2) % 2, (u + 1) % 2, bnext, 0, std::integral_constant<int, 4>{},
-                     [&](int c) { copy_a(pa, ((u + 2) / 2) % 2, 4 + c); });
-            }
+            // Half an A pair, kASlots - 2 pairs further ahead with three
+            // slots: j odd, copies 0..3 of pair kt/2 + ca; j even, copies
+            // 4..7 (the slot is free since this barrier).
+            constexpr int la = kASlots - 2, ca = (u % 2 == 1 ? (u + 3) / 2 : (u + 2) / 2) + la;
+            const uint32_t pa = kt / 2 + ca < npairs ? kt / 2 + ca : npairs - 1;
+            const uint32_t adst = aslot(ca);
+            half(f1, f0, aslot((u + 1) / 2), (u + 1) % 2, bnext, 0, std::integral_constant<int, 4>{},
+                 [&](int c) { copy_a(pa, adst, (u % 2 == 1 ? 0 : 4) + c); });
         };
         uint32_t kt = 0;
         for (; kt + S <= nks; kt += S) {
