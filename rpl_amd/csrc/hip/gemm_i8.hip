@@ -937,8 +937,9 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
 // same swizzle) at a parity offset of 0 or 512 bytes.  B [N,K] pairs use the
 // same layout over BN rows.  B [K,N] (BKN) keeps the per-k-step stages of
 // k_gemm_i8_nt_dma (its rows are whole 256-byte segments already).  LDS: two
-// A pair slots (64 KB), then four B stages (BKN, 64 KB) or three B pair
-// slots (96 KB at BN = 256, 48 KB at 128).
+// A pair slots (64 KB; three, 96 KB, at BN = 128, whose LDS has the room),
+// then four B stages (BKN, 64 KB) or three B pair slots (96 KB at BN = 256,
+// 48 KB at 128).
 //
 // Instruction schedule.  Each 32-k half issues its 4 FN MFMAs with one other
 // memory instruction after each (two after the last ones when there are
@@ -958,10 +959,14 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
 //   second half: MFMAs on k-half 1, reads of tile j+1's k-half 0, and half
 //                an A pair: j odd, copies 0..3 of pair (j+3)/2 into tile j's
 //                pair slot (free since this barrier); j even, copies 4..7 of
-//                pair (j+2)/2.
+//                pair (j+2)/2.  With three A slots the pairs are (j+5)/2 and
+//                (j+4)/2, into the slot of pair (j-1)/2 (free since this
+//                barrier).
 // A B [N,K] pair is complete two iterations before its first read, and the
-// copy count between two waits is the one of the per-k-step B ring, so the
-// waits are the same for both B layouts.  Every iteration issues the same
+// copy count between two waits is the one of the per-k-step B ring, so with
+// two A slots the waits are the same for both B layouts.  With three, the B
+// copies bind: vmcnt(2 kLoadsB + 8) when j is odd, vmcnt(3 kLoadsB + 12)
+// when even.  Every iteration issues the same
 // copies: copies of tiles past the end re-load the last tile (or pair) into
 // a stage or slot that no later read uses, so the wait counts hold to the
 // end and every access stays inside the operands.  Requires K % 128 == 0 and
