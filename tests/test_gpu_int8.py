@@ -271,9 +271,14 @@ def _requant_f32(acc, sa, sb, sc):
 # 256 x 256 kernel (k_gemm_i8_nt<CfgBig>): K = 848 is 13 whole 64-k tiles and
 # a last tile holding 16 k-bytes (the rest zero-filled), K = 592 9 and the
 # same; gemm_int8 reaches it through the transposed copy of B.
+# (1800, 3000, K % 128 == 0) runs the 256 x 128 pairs kernel
+# (k_gemm_i8_pairs_n128: three A pair slots, three B) with ragged M and N:
+# K = 128 is one pair (every later copy clamped to it), 256 two, 384 one
+# 4-k-step round and the remainder, 1152 four rounds and the remainder.
 BIG = [(5890, 5900, 832), (5890, 5888, 832), (6144, 6144, 448), (1800, 3000, 448), (2900, 4400, 448),
        (5890, 5888, 896), (5890, 5900, 896), (2900, 4400, 256), (4096, 3072, 128), (4096, 4096, 64),
-       (6144, 6144, 848), (4096, 8192, 592), (3830, 5104, 1024), (3830, 5110, 1024)]
+       (6144, 6144, 848), (4096, 8192, 592), (3830, 5104, 1024), (3830, 5110, 1024),
+       (1800, 3000, 128), (1800, 3000, 256), (1800, 3000, 384), (1800, 3000, 1152)]
 
 
 @pytest.mark.parametrize("M,N,K", BIG)
