@@ -324,6 +324,19 @@ def test_big_tile_int8_paths(gpu, orc, M, N, K):
     assert bits_equal(got, _requant_f32(acc_zb, 0.013, 0.7, 0.25))
     assert bits_equal(got[rows], orc.gemm_int8(np.ascontiguousarray(A[rows]), B, len(rows), N, K, 0.013, 0.7, 0.25,
                                                0, zb))
+    # Zero points on both sides: acc - zb * rowsum(A) - za * colsum(B) + K * za * zb
+    # (the column term comes from B's column sums, taken with the transposed copy).
+    za = 5
+    out = empty((M, N), np.int32)
+    say("big-tile gemm_int8 za zb", M, N, K)
+    rpl_amd.check(lib.rplhip_gemm_int8(dA.ptr, dB.ptr, out.ptr, M, N, K, 0.013, 0.7, 0.25, za, zb, None))
+    got = down(out, np.int32, (M, N))
+    cs = B.astype(np.int64).sum(0)
+    v = acc.astype(np.int64) - zb * rs[:, None] - za * cs[None, :] + K * za * zb
+    acc_zz = ((v + 2 ** 31) % 2 ** 32 - 2 ** 31).astype(np.int32)
+    assert bits_equal(got, _requant_f32(acc_zz, 0.013, 0.7, 0.25))
+    assert bits_equal(got[rows], orc.gemm_int8(np.ascontiguousarray(A[rows]), B, len(rows), N, K, 0.013, 0.7, 0.25,
+                                               za, zb))
     # gemm_int8_dequant: per-tensor A scale, per-column B scale, B [K,N].
     sa1 = np.float32([0.02])
     sbc = (rng.random(N).astype(np.float32) + 0.5) * np.float32(0.03)
