@@ -985,10 +985,10 @@ __device__ __forceinline__ void gemm_i8_pairs_tile(const int8_t* __restrict__ A,
     using dma::kPairBytes;
     static_assert(BN == 256 || (BN == 128 && !BKN), "B tiles of 256 rows, or 128 rows of B [N,K]");
     constexpr int S = 4, FN = BN / 64, kLoadsB = BN / 64;
-    // B [K,N]: a ring of S k-step stages.  B [N,K]: three k-step pair slots
-    // laid out as A's (BN rows instead of 256).
     // A pair slots: three for 256 x 128 tiles, whose LDS has room (their A
-    // copies then start two k-steps earlier), two for 256 x 256.
+    // copies then start two k-steps earlier), two for 256 x 256.  B [K,N]:
+    // a ring of S k-step stages.  B [N,K]: three k-step pair slots laid out
+    // as A's (BN rows instead of 256).
     constexpr int kASlots = BN == 128 ? 3 : 2;
     constexpr int kBStage = BN * BK, kBPairBytes = BN * 2 * BK, kBBase = kASlots * kPairBytes;
     constexpr int kBBytes = BKN ? S * kBStage : 3 * kBPairBytes;
