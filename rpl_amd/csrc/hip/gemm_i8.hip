@@ -74,11 +74,12 @@ struct EpiParams {
 // The column and row terms of the epilogue, loaded once per column / row by
 // the tile epilogues: cadd (kRaw: bias[n]; kRequant: -za * rowsum_b[n]),
 // cmul (kDequant: sw[n]), radd (kRequant: -zb * rowsum_a[m]) and rmul
-// (kDequant: sx[m]); 0 where the variant has none.
+// (kDequant: sx[m]); 0 where the variant has none.  The int32 products and
+// negations wrap, as the reference's x86 arithmetic does.
 template <int EPI>
 __device__ __forceinline__ int32_t epi_cadd(const EpiParams& p, uint32_t n) {
     if constexpr (EPI == kRaw) return p.bias ? (int32_t)p.bias[n] : 0;
-    if constexpr (EPI == kRequant) return p.rowsum_b ? -wrap_mul(p.za, p.rowsum_b[n]) : 0;
+    if constexpr (EPI == kRequant) return p.rowsum_b ? (int32_t)(0u - (uint32_t)wrap_mul(p.za, p.rowsum_b[n])) : 0;
     return 0;
 }
 template <int EPI>
@@ -88,7 +89,7 @@ __device__ __forceinline__ float epi_cmul(const EpiParams& p, uint32_t n) {
 }
 template <int EPI>
 __device__ __forceinline__ int32_t epi_radd(const EpiParams& p, uint32_t m) {
-    if constexpr (EPI == kRequant) return p.rowsum_a ? -wrap_mul(p.zb, p.rowsum_a[m]) : 0;
+    if constexpr (EPI == kRequant) return p.rowsum_a ? (int32_t)(0u - (uint32_t)wrap_mul(p.zb, p.rowsum_a[m])) : 0;
     return 0;
 }
 template <int EPI>
