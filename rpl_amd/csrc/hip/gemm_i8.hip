@@ -1678,6 +1678,13 @@ bool use_half_tile() {
     return !(env && env[0] == 's');
 }
 
+// One-wave 32 x 32 tiles on small grids unless RPLHIP_I8_SMALL=0 (for A/B
+// timing only).
+bool use_small_tile() {
+    static const char* env = getenv("RPLHIP_I8_SMALL");
+    return !(env && env[0] == '0');
+}
+
 // The direct-to-LDS kernel serves the big tile unless RPLHIP_I8_DMA=0 (for
 // A/B timing only).
 bool use_dma() {
@@ -1747,6 +1754,63 @@ __global__ void __launch_bounds__(256) k_epilogue_k0(uint32_t M, uint32_t N, Epi
     const uint64_t total = (uint64_t)M * N;
     for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (uint64_t)gridDim.x * 256)
         epilogue_store<EPI>(p, (uint32_t)(i / N), (uint32_t)(i % N), 0);
+}
+
+// Small grids with short K (config 1, 512^3: 16 tiles of 128 x 128 for 256
+// CUs): 32 x 32 tiles, one wave each, on v_mfma_i32_32x32x32_i8 with the
+// operand fragments loaded straight from global memory (L2-resident at these
+// sizes) into registers.  Lane l reads, for each 32-k step s, bytes
+// 32s + 16(l/32) .. +15 of row l%32 of A and of B [N,K]: the MFMA's operand
+// layout.  Rows past M / N read the last row (their products are never
+// stored); kSmallDepth steps are in flight, the prefetches past the last
+// whole step re-read it, so no branch sits around a load and the compiler's
+// waits stay exact.  A K % 32 == 16 tail is one more step whose upper k-half
+// is zero.  Requires the aligned layout (16-byte rows, K % 16 == 0).
+constexpr int kSmallDepth = 8;
+constexpr uint32_t kSmallMaxK = 2048;
+template <int EPI>
+__global__ void __launch_bounds__(64) k_gemm_i8_small(const int8_t* __restrict__ A, uint32_t lda,
+                                                      const int8_t* __restrict__ B, uint32_t ldb, uint32_t M,
+                                                      uint32_t N, uint32_t K, EpiParams p) {
+    const uint32_t lane = threadIdx.x;
+    const uint32_t tn = (N + 31) / 32;
+    const uint32_t m0 = (blockIdx.x / tn) * 32, n0 = (blockIdx.x % tn) * 32;
+    const uint32_t ra = m0 + lane % 32 < M ? m0 + lane % 32 : M - 1;
+    const uint32_t rb = n0 + lane % 32 < N ? n0 + lane % 32 : N - 1;
+    const int8_t* arow = A + (uint64_t)ra * lda + 16 * (lane / 32);
+    const int8_t* brow = B + (uint64_t)rb * ldb + 16 * (lane / 32);
+    const uint32_t nkf = K / 32;  // whole 32-k steps
+    v16i acc[1][1] = {};
+    if (nkf > 0) {
+        v4i a[kSmallDepth], b[kSmallDepth];
+        auto load = [&](int d, uint32_t st) {
+            const uint32_t sc = st < nkf ? st : nkf - 1;
+            a[d] = *reinterpret_cast<const v4i*>(arow + 32 * sc);
+            b[d] = *reinterpret_cast<const v4i*>(brow + 32 * sc);
+        };
+#pragma unroll
+        for (int d = 0; d < kSmallDepth; d++) load(d, d);
+        uint32_t st = 0;
+        for (; st + kSmallDepth <= nkf; st += kSmallDepth) {
+#pragma unroll
+            for (int d = 0; d < kSmallDepth; d++) {
+                acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[d], b[d], acc[0][0], 0, 0, 0);
+                load(d, st + kSmallDepth + d);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < kSmallDepth; d++)
+            if (st + d < nkf) acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[d], b[d], acc[0][0], 0, 0, 0);
+    }
+    if (K % 32) {
+        v4i a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
+        if (lane < 32) {
+            a = *reinterpret_cast<const v4i*>(arow + 32 * nkf);
+            b = *reinterpret_cast<const v4i*>(brow + 32 * nkf);
+        }
+        acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[0][0], 0, 0, 0);
+    }
+    epilogue_tile<EPI, 1, 1>(p, acc, m0 + 4 * (lane / 32), n0 + lane % 32, M, N);
 }
 
 template <int EPI>
@@ -1864,6 +1928,16 @@ int run_nt(const int8_t* A, uint32_t lda, const int8_t* B, uint32_t ldb, uint32_
             hipLaunchKernelGGL((k_gemm_i8_nt_dma<EPI, 128>), dim3((uint32_t)tiles_half), dim3(dma::kThreads), 0, s, A,
                                lda, B, ldb, M, N, K, p);
         return rplhip::check_launch("int8 GEMM");
+    }
+    // 128 x 128 tiles for fewer than a quarter of the CUs and a short K: one
+    // wave per 32 x 32 tile instead (512^3: 256 waves against 16 blocks,
+    // 7.45 -> 3.69 us; at 1024^2, 64 tiles, the 128 x 128 kernel is faster).
+    const uint64_t tiles128 = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
+    const uint64_t tiles32 = (uint64_t)((M + 31) / 32) * ((N + 31) / 32);
+    if (al && K <= kSmallMaxK && 4 * tiles128 < rplhip::cu_count() && use_small_tile()) {
+        hipLaunchKernelGGL((k_gemm_i8_small<EPI>), dim3((uint32_t)tiles32), dim3(64), 0, s, A, lda, B, ldb, M, N, K,
+                           p);
+        return rplhip::check_launch("int8 GEMM (small grid)");
     }
     return launch_nt<CfgSmall, EPI>(A, lda, B, ldb, M, N, K, p, al, s);
 }

@@ -76,6 +76,38 @@ def test_linear_int8_vs_oracle(gpu, orc, M, K, N):
     assert bits_equal(linear_int8(x, w, None, M, K, N), orc.linear_int8(x, w, None, M, K, N))
 
 
+# Small grids with short K take one wave per 32 x 32 tile (k_gemm_i8_small):
+# ragged M and N, K % 32 == 16 (a last half step whose upper k-half is zero;
+# K = 16 is that step alone), fewer k-steps than the 8 in flight, and the
+# K = 2048 limit; raw with and without bias, requant with zero points on both
+# sides (B's column sums from the transposed copy), and both dequant entry
+# points, all bit-exact against the oracle.
+@pytest.mark.parametrize("M,N,K", [(33, 65, 16), (96, 80, 48), (17, 40, 160), (100, 200, 1040), (257, 31, 2048),
+                                   (512, 512, 512)])
+def test_small_grid_int8_vs_oracle(gpu, orc, M, N, K):
+    rng = np.random.default_rng(M * 5 + N + K)
+    x = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    b = rng.integers(-128, 128, N, dtype=np.int8)
+    say("small-grid linear_int8", M, N, K)
+    assert bits_equal(linear_int8(x, w, b, M, K, N), orc.linear_int8(x, w, b, M, K, N))
+    acc = orc.linear_int8(x, w, None, M, K, N)
+    assert bits_equal(linear_int8(x, w, None, M, K, N), acc)
+    B = np.ascontiguousarray(w.T)
+    for (sa, sb, sc, za, zb) in ((1.0, 1.0, 1.0, 0, 0), (0.013, 0.7, 0.29, -3, 11)):
+        say("small-grid gemm_int8", M, N, K, za, zb)
+        assert bits_equal(gemm_int8(x, B, M, N, K, sa, sb, sc, za, zb), orc.gemm_int8(x, B, M, N, K, sa, sb, sc, za, zb))
+    sx = rng.random(M).astype(np.float32) * 0.01
+    sw = rng.random(N).astype(np.float32) * 0.02
+    say("small-grid linear_int8_dequant", M, N, K)
+    assert bits_equal(linear_int8_dequant(x, sx, True, w, sw, True, M, K, N), orc.dequant_acc(acc, sx, True, sw, True))
+    lib = gpu
+    dx, dB, dsa, dsw, dY = up(x), up(B), up(sx[:1]), up(sw), empty((M, N), np.float32)
+    say("small-grid gemm_int8_dequant", M, N, K)
+    rpl_amd.check(lib.rplhip_gemm_int8_dequant(dx.ptr, dsa.ptr, 0, dB.ptr, dsw.ptr, 1, dY.ptr, M, N, K, None))
+    assert bits_equal(down(dY, np.float32, (M, N)), orc.dequant_acc(acc, sx[:1], False, sw, True))
+
+
 # K = 0: every accumulator is the empty sum, so the outputs are the epilogue
 # of 0 (requant of 0, sc = 0 -> 0/0 -> INT32_MIN, bias alone, 0 * scales).
 # 4096 x 4096 is a grid the big-tile kernels would otherwise take.
