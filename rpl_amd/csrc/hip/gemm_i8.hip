@@ -927,7 +927,8 @@ __global__ void __launch_bounds__(256, 1) k_gemm_i8_nt_dma(const int8_t* __restr
 // [N,K], copied in k-step pairs: one copy instruction moves 8 rows x 128
 // bytes (8 whole cache lines; the per-k-step copy moves 16 rows x 64 bytes,
 // half of 16 lines, and fetches each line twice; whole lines copy 1.5-1.75x
-// faster from L2, MALL and HBM alike, measured on MI355X).  A pair of A tiles
+// faster than half lines under the same access pattern, measured on
+// MI355X).  A pair of A tiles
 // fills a 32 KB region laid out in 1 KB row groups: group g holds rows
 // 8g..8g+7, the first 512 bytes k-step 2p, the next 512 bytes k-step 2p+1,
 // each as 8 rows x 64 bytes with chunk c at slot c ^ swz(row).  Lane l of a
